@@ -1,0 +1,190 @@
+"""Drop-in Python binding for the MI355X GDN kernels (destination-passing style).
+
+Mirrors the reference's entry points argument for argument:
+
+* ``decode_kernel(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state)``
+  -- the TVM-FFI ``kernel`` of solution/cuda/kernel.cu:101-113,150 (also the
+  Triton ``kernel`` of solution/triton/kernel.py:61).
+* ``prefill_kernel(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale,
+  output, new_state)`` -- the TVM-FFI ``kernel`` of
+  solution/cuda/kernel_prefill.cu:300-306,339.
+* ``decode_pooled_kernel(q, k, v, state_pool, A_log, a, dt_bias, b, scale,
+  output, state_indices)`` -- no reference counterpart; decode over an indexed
+  state pool, updated in place.
+
+Semantics kept from the reference: outputs are preallocated and written in
+place; ``scale`` None or 0 selects 1/sqrt(dk); ``state`` None means a zero
+initial state; ``new_state`` may be the same tensor as ``state``; launches are
+asynchronous on the current stream.  Unlike the reference (which checks
+nothing), shapes, dtypes, devices and contiguity are validated and reported as
+``ValueError``; device errors raise ``GDNError``.
+
+Tensors travel to the C ABI as raw device pointers; torch is used only for
+tensor metadata and the current HIP stream.
+"""
+from __future__ import annotations
+
+from typing import Optional
+
+import torch
+
+from . import _lib
+
+__all__ = ["decode_kernel", "decode_pooled_kernel", "prefill_kernel", "GDNError"]
+
+GDNError = _lib.GDNError
+_BF16 = torch.bfloat16
+_F32 = torch.float32
+
+
+def _need(t: torch.Tensor, name: str, dtype: torch.dtype, shape: tuple, device) -> None:
+    if not isinstance(t, torch.Tensor):
+        raise ValueError(f"{name} must be a torch.Tensor")
+    if t.dtype != dtype:
+        raise ValueError(f"{name} must be {dtype} (got {t.dtype})")
+    if tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name} must have shape {tuple(shape)} (got {tuple(t.shape)})")
+    if t.device != device:
+        raise ValueError(f"{name} is on {t.device}, expected {device}")
+    if not t.is_contiguous():
+        raise ValueError(f"{name} must be contiguous")
+
+
+def _device_of(q: torch.Tensor) -> torch.device:
+    if not isinstance(q, torch.Tensor):
+        raise ValueError("q must be a torch.Tensor")
+    if q.device.type != "cuda":
+        raise ValueError(f"tensors must be on a ROCm GPU device (got {q.device})")
+    return q.device
+
+
+def _ptr(t: Optional[torch.Tensor]) -> Optional[int]:
+    return None if t is None or t.numel() == 0 else t.data_ptr()
+
+
+def _scale(scale) -> float:
+    return 0.0 if scale is None else float(scale)
+
+
+def _stream(device: torch.device) -> int:
+    return torch.cuda.current_stream(device).cuda_stream
+
+
+def decode_kernel(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state) -> None:
+    """GDN decode step (T = 1).  Shapes (design.md:97-121):
+    q,k [B,1,H{q,k},128] bf16; v [B,1,Hv,128] bf16; state [B,Hv,128,128] fp32 or
+    None; A_log,dt_bias [Hv] fp32; a,b [B,1,Hv] bf16; output [B,1,Hv,128] bf16;
+    new_state [B,Hv,128,128] fp32 (may be ``state``)."""
+    dev = _device_of(q)
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+        raise ValueError("q, k, v must be 4-D [B, 1, H, d]")
+    B, T, Hq, dk = q.shape
+    Hk = k.shape[2]
+    Hv, dv = v.shape[2], v.shape[3]
+    if T != 1:
+        raise ValueError(f"decode expects T == 1 (got {T})")
+    _need(q, "q", _BF16, (B, 1, Hq, dk), dev)
+    _need(k, "k", _BF16, (B, 1, Hk, dk), dev)
+    _need(v, "v", _BF16, (B, 1, Hv, dv), dev)
+    if state is not None:
+        _need(state, "state", _F32, (B, Hv, dv, dk), dev)
+    _need(A_log, "A_log", _F32, (Hv,), dev)
+    _need(a, "a", _BF16, (B, 1, Hv), dev)
+    _need(dt_bias, "dt_bias", _F32, (Hv,), dev)
+    _need(b, "b", _BF16, (B, 1, Hv), dev)
+    _need(output, "output", _BF16, (B, 1, Hv, dv), dev)
+    _need(new_state, "new_state", _F32, (B, Hv, dv, dk), dev)
+    lib = _lib.load()
+    with torch.cuda.device(dev):
+        rc = lib.gdn_decode(_ptr(q), _ptr(k), _ptr(v), _ptr(state), _ptr(A_log), _ptr(a),
+                            _ptr(dt_bias), _ptr(b), _scale(scale), _ptr(output), _ptr(new_state),
+                            B, Hq, Hk, Hv, dk, dv, _stream(dev))
+    _lib.check(rc)
+
+
+def decode_pooled_kernel(q, k, v, state_pool, A_log, a, dt_bias, b, scale, output,
+                         state_indices) -> None:
+    """Decode step with the state of batch row i held in ``state_pool[state_indices[i]]``
+    (updated in place).  state_pool [S,Hv,128,128] fp32; state_indices [B] int32;
+    an index outside [0, S) is a padding row (zero output, no slot touched).
+    Valid indices must be distinct."""
+    dev = _device_of(q)
+    if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
+        raise ValueError("q, k, v must be 4-D [B, 1, H, d]")
+    B, T, Hq, dk = q.shape
+    Hk = k.shape[2]
+    Hv, dv = v.shape[2], v.shape[3]
+    if T != 1:
+        raise ValueError(f"decode expects T == 1 (got {T})")
+    if state_pool.dim() != 4:
+        raise ValueError("state_pool must be 4-D [slots, Hv, dv, dk]")
+    slots = state_pool.shape[0]
+    _need(q, "q", _BF16, (B, 1, Hq, dk), dev)
+    _need(k, "k", _BF16, (B, 1, Hk, dk), dev)
+    _need(v, "v", _BF16, (B, 1, Hv, dv), dev)
+    _need(state_pool, "state_pool", _F32, (slots, Hv, dv, dk), dev)
+    _need(state_indices, "state_indices", torch.int32, (B,), dev)
+    _need(A_log, "A_log", _F32, (Hv,), dev)
+    _need(a, "a", _BF16, (B, 1, Hv), dev)
+    _need(dt_bias, "dt_bias", _F32, (Hv,), dev)
+    _need(b, "b", _BF16, (B, 1, Hv), dev)
+    _need(output, "output", _BF16, (B, 1, Hv, dv), dev)
+    lib = _lib.load()
+    with torch.cuda.device(dev):
+        rc = lib.gdn_decode_pooled(_ptr(q), _ptr(k), _ptr(v), _ptr(state_pool), slots,
+                                   _ptr(state_indices), _ptr(A_log), _ptr(a), _ptr(dt_bias),
+                                   _ptr(b), _scale(scale), _ptr(output), B, Hq, Hk, Hv, dk, dv,
+                                   _stream(dev))
+    _lib.check(rc)
+
+
+def prefill_kernel(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output,
+                   new_state) -> None:
+    """Varlen chunked prefill over packed sequences (kernel_prefill.cu:300-306).
+    q,k [T,H{q,k},128] bf16 (a leading batch dim of 1 is accepted); v [T,Hv,128]
+    bf16; state [N,Hv,128,128] fp32 or None; a,b [T,Hv] bf16; cu_seqlens [N+1]
+    int32 or int64 on the device; output [T,Hv,128] bf16; new_state
+    [N,Hv,128,128] fp32 (may be ``state``)."""
+    dev = _device_of(q)
+
+    def squeeze1(t, name, nd):
+        if t is not None and t.dim() == nd + 1 and t.shape[0] == 1:
+            return t[0]
+        return t
+
+    q, k, v = squeeze1(q, "q", 3), squeeze1(k, "k", 3), squeeze1(v, "v", 3)
+    a, b, output = squeeze1(a, "a", 2), squeeze1(b, "b", 2), squeeze1(output, "output", 3)
+    if q.dim() != 3 or k.dim() != 3 or v.dim() != 3:
+        raise ValueError("q, k, v must be [T, H, d] (optionally with a leading 1)")
+    T, Hq, dk = q.shape
+    Hk = k.shape[1]
+    Hv, dv = v.shape[1], v.shape[2]
+    if not isinstance(cu_seqlens, torch.Tensor) or cu_seqlens.dim() != 1 or cu_seqlens.numel() < 1:
+        raise ValueError("cu_seqlens must be a 1-D tensor [N + 1]")
+    if cu_seqlens.dtype == torch.int32:
+        cu_code = _lib.GDN_INDEX_INT32
+    elif cu_seqlens.dtype == torch.int64:
+        cu_code = _lib.GDN_INDEX_INT64
+    else:
+        raise ValueError(f"cu_seqlens must be int32 or int64 (got {cu_seqlens.dtype})")
+    if cu_seqlens.device != dev or not cu_seqlens.is_contiguous():
+        raise ValueError("cu_seqlens must be contiguous and on the same device as q")
+    N = cu_seqlens.numel() - 1
+    _need(q, "q", _BF16, (T, Hq, dk), dev)
+    _need(k, "k", _BF16, (T, Hk, dk), dev)
+    _need(v, "v", _BF16, (T, Hv, dv), dev)
+    if state is not None:
+        _need(state, "state", _F32, (N, Hv, dv, dk), dev)
+    _need(A_log, "A_log", _F32, (Hv,), dev)
+    _need(a, "a", _BF16, (T, Hv), dev)
+    _need(dt_bias, "dt_bias", _F32, (Hv,), dev)
+    _need(b, "b", _BF16, (T, Hv), dev)
+    _need(output, "output", _BF16, (T, Hv, dv), dev)
+    _need(new_state, "new_state", _F32, (N, Hv, dv, dk), dev)
+    lib = _lib.load()
+    with torch.cuda.device(dev):
+        rc = lib.gdn_prefill(_ptr(q), _ptr(k), _ptr(v), _ptr(state), _ptr(A_log), _ptr(a),
+                             _ptr(dt_bias), _ptr(b), cu_seqlens.data_ptr(), cu_code, N, T,
+                             _scale(scale), _ptr(output), _ptr(new_state), Hq, Hk, Hv, dk, dv,
+                             _stream(dev))
+    _lib.check(rc)

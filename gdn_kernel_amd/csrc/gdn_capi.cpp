@@ -1,0 +1,201 @@
+// C-ABI entry points: argument validation (host only, no device calls) and
+// dispatch to the kernel launchers.
+#include <hip/hip_runtime.h>
+
+#include <cmath>
+#include <cstdarg>
+#include <cstdio>
+#include <cstring>
+
+#include "../../include/gdn_kernel_amd.h"
+#include "gdn_launch.hpp"
+
+namespace {
+
+thread_local char g_err[512] = "";
+
+int fail(int code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+int ok() {
+  g_err[0] = '\0';
+  return GDN_OK;
+}
+
+constexpr int kD = 128;
+constexpr int64_t kMaxGrid = 0x7fffffff;
+
+int check_heads(int32_t hq, int32_t hk, int32_t hv, int32_t dk, int32_t dv) {
+  if (hq <= 0 || hk <= 0 || hv <= 0)
+    return fail(GDN_ERR_INVALID_ARGUMENT, "head counts must be positive (Hq=%d Hk=%d Hv=%d)", hq, hk, hv);
+  if (hv % hq != 0 || hv % hk != 0)
+    return fail(GDN_ERR_INVALID_ARGUMENT,
+                "num_v_heads (%d) must be a multiple of num_q_heads (%d) and num_k_heads (%d)", hv, hq, hk);
+  if (dk <= 0 || dv <= 0)
+    return fail(GDN_ERR_INVALID_ARGUMENT, "head dims must be positive (dk=%d dv=%d)", dk, dv);
+  if (dk != kD || dv != kD)
+    return fail(GDN_ERR_UNSUPPORTED, "only head_dim_k == head_dim_v == 128 is implemented (got %d, %d)", dk, dv);
+  return GDN_OK;
+}
+
+int check_scale(double scale) {
+  if (!std::isfinite(scale)) return fail(GDN_ERR_INVALID_ARGUMENT, "scale must be finite");
+  return GDN_OK;
+}
+
+float resolve_scale(double scale) {
+  return scale == 0.0 ? 1.0f / std::sqrt(float(kD)) : float(scale);
+}
+
+// new_state may equal state (in place) but must not partially overlap it.
+int check_alias(const void* in, const void* out, int64_t bytes, const char* what) {
+  if (!in || !out || in == out || bytes <= 0) return GDN_OK;
+  const char* a = static_cast<const char*>(in);
+  const char* b = static_cast<const char*>(out);
+  if (a < b + bytes && b < a + bytes)
+    return fail(GDN_ERR_INVALID_ARGUMENT, "%s partially overlaps its input (only exact aliasing is allowed)", what);
+  return GDN_OK;
+}
+
+#define GDN_TRY(expr)            \
+  do {                           \
+    const int rc_ = (expr);      \
+    if (rc_ != GDN_OK) return rc_; \
+  } while (0)
+
+int device_status(hipError_t e, const char* what) {
+  if (e != hipSuccess) return fail(GDN_ERR_DEVICE, "%s: %s", what, hipGetErrorString(e));
+  return ok();
+}
+
+}  // namespace
+
+extern "C" {
+
+int gdn_version(void) { return 100; }
+
+const char* gdn_last_error(void) { return g_err; }
+
+int gdn_decode_check(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v, const float* state,
+                     const float* A_log, const gdn_bf16* a, const float* dt_bias, const gdn_bf16* b,
+                     double scale, gdn_bf16* output, float* new_state, int64_t batch, int32_t num_q_heads,
+                     int32_t num_k_heads, int32_t num_v_heads, int32_t head_dim_k, int32_t head_dim_v) {
+  if (batch < 0) return fail(GDN_ERR_INVALID_ARGUMENT, "batch must be >= 0 (got %lld)", (long long)batch);
+  GDN_TRY(check_heads(num_q_heads, num_k_heads, num_v_heads, head_dim_k, head_dim_v));
+  GDN_TRY(check_scale(scale));
+  if (batch == 0) return ok();
+  if (!q || !k || !v || !A_log || !a || !dt_bias || !b || !output || !new_state)
+    return fail(GDN_ERR_INVALID_ARGUMENT, "null tensor pointer (only state may be null)");
+  if (batch * num_v_heads * (kD / 8) > kMaxGrid)
+    return fail(GDN_ERR_INVALID_ARGUMENT, "batch * num_v_heads too large (%lld)", (long long)(batch * num_v_heads));
+  GDN_TRY(check_alias(state, new_state, batch * num_v_heads * int64_t(kD) * kD * 4, "new_state"));
+  return ok();
+}
+
+int gdn_decode(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v, const float* state,
+               const float* A_log, const gdn_bf16* a, const float* dt_bias, const gdn_bf16* b, double scale,
+               gdn_bf16* output, float* new_state, int64_t batch, int32_t num_q_heads, int32_t num_k_heads,
+               int32_t num_v_heads, int32_t head_dim_k, int32_t head_dim_v, void* stream) {
+  GDN_TRY(gdn_decode_check(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state, batch, num_q_heads,
+                           num_k_heads, num_v_heads, head_dim_k, head_dim_v));
+  if (batch == 0) return ok();
+  gdn::DecodeArgs args{};
+  args.q = q; args.k = k; args.v = v;
+  args.state = state; args.new_state = new_state;
+  args.A_log = A_log; args.a = a; args.dt_bias = dt_bias; args.b = b;
+  args.slots = nullptr; args.pool_slots = 0;
+  args.out = output;
+  args.scale = resolve_scale(scale);
+  args.B = int(batch); args.Hq = num_q_heads; args.Hk = num_k_heads; args.Hv = num_v_heads;
+  return device_status(gdn::launch_decode(args, static_cast<hipStream_t>(stream)), "gdn_decode launch");
+}
+
+int gdn_decode_pooled_check(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v, float* state_pool,
+                            int64_t pool_slots, const int32_t* state_indices, const float* A_log,
+                            const gdn_bf16* a, const float* dt_bias, const gdn_bf16* b, double scale,
+                            gdn_bf16* output, int64_t batch, int32_t num_q_heads, int32_t num_k_heads,
+                            int32_t num_v_heads, int32_t head_dim_k, int32_t head_dim_v) {
+  if (batch < 0) return fail(GDN_ERR_INVALID_ARGUMENT, "batch must be >= 0 (got %lld)", (long long)batch);
+  if (pool_slots <= 0) return fail(GDN_ERR_INVALID_ARGUMENT, "pool_slots must be > 0 (got %lld)", (long long)pool_slots);
+  GDN_TRY(check_heads(num_q_heads, num_k_heads, num_v_heads, head_dim_k, head_dim_v));
+  GDN_TRY(check_scale(scale));
+  if (batch == 0) return ok();
+  if (!q || !k || !v || !state_pool || !state_indices || !A_log || !a || !dt_bias || !b || !output)
+    return fail(GDN_ERR_INVALID_ARGUMENT, "null tensor pointer");
+  if (batch * num_v_heads * (kD / 8) > kMaxGrid)
+    return fail(GDN_ERR_INVALID_ARGUMENT, "batch * num_v_heads too large (%lld)", (long long)(batch * num_v_heads));
+  return ok();
+}
+
+int gdn_decode_pooled(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v, float* state_pool,
+                      int64_t pool_slots, const int32_t* state_indices, const float* A_log, const gdn_bf16* a,
+                      const float* dt_bias, const gdn_bf16* b, double scale, gdn_bf16* output, int64_t batch,
+                      int32_t num_q_heads, int32_t num_k_heads, int32_t num_v_heads, int32_t head_dim_k,
+                      int32_t head_dim_v, void* stream) {
+  GDN_TRY(gdn_decode_pooled_check(q, k, v, state_pool, pool_slots, state_indices, A_log, a, dt_bias, b, scale,
+                                  output, batch, num_q_heads, num_k_heads, num_v_heads, head_dim_k, head_dim_v));
+  if (batch == 0) return ok();
+  gdn::DecodeArgs args{};
+  args.q = q; args.k = k; args.v = v;
+  args.state = state_pool; args.new_state = state_pool;
+  args.A_log = A_log; args.a = a; args.dt_bias = dt_bias; args.b = b;
+  args.slots = state_indices; args.pool_slots = pool_slots;
+  args.out = output;
+  args.scale = resolve_scale(scale);
+  args.B = int(batch); args.Hq = num_q_heads; args.Hk = num_k_heads; args.Hv = num_v_heads;
+  return device_status(gdn::launch_decode(args, static_cast<hipStream_t>(stream)), "gdn_decode_pooled launch");
+}
+
+int gdn_prefill_check(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v, const float* state,
+                      const float* A_log, const gdn_bf16* a, const float* dt_bias, const gdn_bf16* b,
+                      const void* cu_seqlens, int32_t cu_seqlens_dtype, int64_t num_seqs, int64_t total_tokens,
+                      double scale, gdn_bf16* output, float* new_state, int32_t num_q_heads, int32_t num_k_heads,
+                      int32_t num_v_heads, int32_t head_dim_k, int32_t head_dim_v) {
+  if (num_seqs < 0) return fail(GDN_ERR_INVALID_ARGUMENT, "num_seqs must be >= 0 (got %lld)", (long long)num_seqs);
+  if (total_tokens < 0)
+    return fail(GDN_ERR_INVALID_ARGUMENT, "total_tokens must be >= 0 (got %lld)", (long long)total_tokens);
+  if (total_tokens > kMaxGrid)
+    return fail(GDN_ERR_INVALID_ARGUMENT, "total_tokens too large (%lld)", (long long)total_tokens);
+  if (cu_seqlens_dtype != GDN_INDEX_INT32 && cu_seqlens_dtype != GDN_INDEX_INT64)
+    return fail(GDN_ERR_INVALID_ARGUMENT, "cu_seqlens_dtype must be GDN_INDEX_INT32 or GDN_INDEX_INT64 (got %d)",
+                cu_seqlens_dtype);
+  GDN_TRY(check_heads(num_q_heads, num_k_heads, num_v_heads, head_dim_k, head_dim_v));
+  GDN_TRY(check_scale(scale));
+  if (num_seqs == 0) return ok();
+  if (num_seqs * num_v_heads > kMaxGrid)
+    return fail(GDN_ERR_INVALID_ARGUMENT, "num_seqs * num_v_heads too large");
+  if (!cu_seqlens || !A_log || !dt_bias || !new_state)
+    return fail(GDN_ERR_INVALID_ARGUMENT, "null tensor pointer (only state may be null)");
+  if (total_tokens > 0 && (!q || !k || !v || !a || !b || !output))
+    return fail(GDN_ERR_INVALID_ARGUMENT, "null tensor pointer (only state may be null)");
+  GDN_TRY(check_alias(state, new_state, num_seqs * num_v_heads * int64_t(kD) * kD * 4, "new_state"));
+  return ok();
+}
+
+int gdn_prefill(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v, const float* state, const float* A_log,
+                const gdn_bf16* a, const float* dt_bias, const gdn_bf16* b, const void* cu_seqlens,
+                int32_t cu_seqlens_dtype, int64_t num_seqs, int64_t total_tokens, double scale, gdn_bf16* output,
+                float* new_state, int32_t num_q_heads, int32_t num_k_heads, int32_t num_v_heads,
+                int32_t head_dim_k, int32_t head_dim_v, void* stream) {
+  GDN_TRY(gdn_prefill_check(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu_seqlens_dtype, num_seqs,
+                            total_tokens, scale, output, new_state, num_q_heads, num_k_heads, num_v_heads,
+                            head_dim_k, head_dim_v));
+  if (num_seqs == 0) return ok();
+  gdn::PrefillArgs args{};
+  args.q = q; args.k = k; args.v = v;
+  args.state = state; args.new_state = new_state;
+  args.A_log = A_log; args.a = a; args.dt_bias = dt_bias; args.b = b;
+  args.cu_seqlens = cu_seqlens; args.cu_is_64 = cu_seqlens_dtype == GDN_INDEX_INT64;
+  args.out = output;
+  args.scale = resolve_scale(scale);
+  args.T = total_tokens;
+  args.N = int(num_seqs); args.Hq = num_q_heads; args.Hk = num_k_heads; args.Hv = num_v_heads;
+  return device_status(gdn::launch_prefill(args, static_cast<hipStream_t>(stream)), "gdn_prefill launch");
+}
+
+}  // extern "C"

@@ -1,0 +1,48 @@
+// Internal launcher interface between the C-ABI layer (gdn_capi.cpp) and the
+// kernel translation units.  Arguments here are already validated.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace gdn {
+
+struct DecodeArgs {
+  const uint16_t* q;        // [B, Hq, 128] bf16
+  const uint16_t* k;        // [B, Hk, 128] bf16
+  const uint16_t* v;        // [B, Hv, 128] bf16
+  const float* state;       // [B|slots, Hv, 128, 128]; null => zero initial state
+  float* new_state;         // same layout; may alias state
+  const float* A_log;       // [Hv]
+  const uint16_t* a;        // [B, Hv] bf16
+  const float* dt_bias;     // [Hv]
+  const uint16_t* b;        // [B, Hv] bf16
+  const int32_t* slots;     // pooled mode: state head block = slots[bi]; else null
+  int64_t pool_slots;       // pooled mode: number of slots in the pool
+  uint16_t* out;            // [B, Hv, 128] bf16
+  float scale;
+  int B, Hq, Hk, Hv;
+};
+
+struct PrefillArgs {
+  const uint16_t* q;        // [T, Hq, 128] bf16
+  const uint16_t* k;        // [T, Hk, 128] bf16
+  const uint16_t* v;        // [T, Hv, 128] bf16
+  const float* state;       // [N, Hv, 128, 128] initial states; null => zeros
+  float* new_state;         // [N, Hv, 128, 128] final states; may alias state
+  const float* A_log;       // [Hv]
+  const uint16_t* a;        // [T, Hv] bf16
+  const float* dt_bias;     // [Hv]
+  const uint16_t* b;        // [T, Hv] bf16
+  const void* cu_seqlens;   // [N + 1] int32 or int64
+  int cu_is_64;             // 1 => int64 cu_seqlens
+  uint16_t* out;            // [T, Hv, 128] bf16
+  float scale;
+  int64_t T;                // total packed tokens
+  int N, Hq, Hk, Hv;
+};
+
+hipError_t launch_decode(const DecodeArgs& args, hipStream_t stream);
+hipError_t launch_prefill(const PrefillArgs& args, hipStream_t stream);
+
+}  // namespace gdn

@@ -1,0 +1,137 @@
+/*
+ * gdn_kernel_amd -- C ABI of the MI355X (gfx950) Gated DeltaNet decode and
+ * varlen chunked prefill kernels.
+ *
+ * Every entry point takes raw device pointers, explicit sizes and a HIP stream
+ * passed as an opaque pointer (hipStream_t; NULL = the default stream).  All
+ * tensors are dense row-major (C-contiguous) in the layouts documented per
+ * function; bf16 tensors are raw 16-bit bf16 bit patterns.  Launches are
+ * asynchronous on the given stream; no entry point synchronises, allocates
+ * device memory or keeps state between calls.
+ *
+ * Return value: GDN_OK (0) on success, otherwise a GDN_ERR_* code; the
+ * calling thread's gdn_last_error() then describes the failure.  Argument
+ * validation happens before any device call, so invalid arguments are reported
+ * without touching a GPU.
+ *
+ * Head dims: dk = dv = 128.  GQA: v-head h reads q-head h / (Hv/Hq) and k-head
+ * h / (Hv/Hk); Hv must be a multiple of Hq and of Hk.
+ * scale == 0 selects the default 1/sqrt(dk).
+ */
+#ifndef GDN_KERNEL_AMD_H
+#define GDN_KERNEL_AMD_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef uint16_t gdn_bf16; /* raw bf16 bits */
+
+#define GDN_OK 0
+#define GDN_ERR_INVALID_ARGUMENT 1 /* bad pointer, size, head ratio, dtype code */
+#define GDN_ERR_UNSUPPORTED 2      /* valid request this build does not implement */
+#define GDN_ERR_DEVICE 3           /* HIP launch / runtime error */
+
+#define GDN_INDEX_INT32 0
+#define GDN_INDEX_INT64 1
+
+/* Library version, as MAJOR*10000 + MINOR*100 + PATCH. */
+int gdn_version(void);
+
+/* Message describing the last failure on the calling thread ("" if none). */
+const char* gdn_last_error(void);
+
+/*
+ * Decode step, destination-passing.  Replaces the reference's TVM-FFI export
+ * `kernel` = GDNDecodeKernel (solution/cuda/kernel.cu:101-113, exported at
+ * :150), same argument order: q, k, v, state, A_log, a, dt_bias, b, scale,
+ * output, new_state.
+ *   q [B,1,Hq,128] bf16, k [B,1,Hk,128] bf16, v [B,1,Hv,128] bf16
+ *   state     [B,Hv,128,128] fp32, or NULL for a zero initial state
+ *             (the reference memsets new_state and aliases it, kernel.cu:135-139)
+ *   A_log [Hv] fp32, a [B,1,Hv] bf16, dt_bias [Hv] fp32, b [B,1,Hv] bf16
+ *   output    [B,1,Hv,128] bf16
+ *   new_state [B,Hv,128,128] fp32; may be the same pointer as state (in place)
+ */
+int gdn_decode(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v,
+               const float* state, const float* A_log, const gdn_bf16* a,
+               const float* dt_bias, const gdn_bf16* b, double scale,
+               gdn_bf16* output, float* new_state, int64_t batch,
+               int32_t num_q_heads, int32_t num_k_heads, int32_t num_v_heads,
+               int32_t head_dim_k, int32_t head_dim_v, void* stream);
+
+/* Validation of gdn_decode's arguments only; touches no device. */
+int gdn_decode_check(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v,
+                     const float* state, const float* A_log, const gdn_bf16* a,
+                     const float* dt_bias, const gdn_bf16* b, double scale,
+                     gdn_bf16* output, float* new_state, int64_t batch,
+                     int32_t num_q_heads, int32_t num_k_heads, int32_t num_v_heads,
+                     int32_t head_dim_k, int32_t head_dim_v);
+
+/*
+ * Decode step over an indexed state pool, updated in place.  No reference
+ * counterpart: it is the reference decode (kernel.cu:101-148) with the state
+ * of batch row i read from and written back to pool slot state_indices[i].
+ *   state_pool    [pool_slots,Hv,128,128] fp32 (read and written)
+ *   state_indices [B] int32 device array; an index outside [0, pool_slots)
+ *                 marks a padding row: its output is zero and no slot is touched.
+ * Two valid rows naming the same slot race; callers must not do that.
+ * Other arguments as gdn_decode.
+ */
+int gdn_decode_pooled(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v,
+                      float* state_pool, int64_t pool_slots,
+                      const int32_t* state_indices, const float* A_log,
+                      const gdn_bf16* a, const float* dt_bias, const gdn_bf16* b,
+                      double scale, gdn_bf16* output, int64_t batch,
+                      int32_t num_q_heads, int32_t num_k_heads, int32_t num_v_heads,
+                      int32_t head_dim_k, int32_t head_dim_v, void* stream);
+
+int gdn_decode_pooled_check(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v,
+                            float* state_pool, int64_t pool_slots,
+                            const int32_t* state_indices, const float* A_log,
+                            const gdn_bf16* a, const float* dt_bias, const gdn_bf16* b,
+                            double scale, gdn_bf16* output, int64_t batch,
+                            int32_t num_q_heads, int32_t num_k_heads,
+                            int32_t num_v_heads, int32_t head_dim_k,
+                            int32_t head_dim_v);
+
+/*
+ * Varlen chunked prefill (chunk 64), destination-passing.  Replaces the
+ * reference's TVM-FFI export `kernel` = GDNPrefillKernel
+ * (solution/cuda/kernel_prefill.cu:300-306, exported at :339), same argument
+ * order: q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output,
+ * new_state.
+ *   q [T,Hq,128] bf16, k [T,Hk,128] bf16, v [T,Hv,128] bf16 (packed tokens)
+ *   state     [N,Hv,128,128] fp32 initial states, or NULL for zeros
+ *   A_log [Hv] fp32, a [T,Hv] bf16, dt_bias [Hv] fp32, b [T,Hv] bf16
+ *   cu_seqlens [N+1] device array, GDN_INDEX_INT32 or GDN_INDEX_INT64
+ *             (the reference takes int64, kernel_prefill.cu:46); sequence i is
+ *             tokens [cu[i], cu[i+1]).  An empty sequence passes its initial
+ *             state through.  Entries are clamped into [0, T] on the device,
+ *             so malformed offsets cannot make the kernel read out of bounds.
+ *   output    [T,Hv,128] bf16
+ *   new_state [N,Hv,128,128] fp32 final states; may alias state.
+ */
+int gdn_prefill(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v,
+                const float* state, const float* A_log, const gdn_bf16* a,
+                const float* dt_bias, const gdn_bf16* b, const void* cu_seqlens,
+                int32_t cu_seqlens_dtype, int64_t num_seqs, int64_t total_tokens,
+                double scale, gdn_bf16* output, float* new_state,
+                int32_t num_q_heads, int32_t num_k_heads, int32_t num_v_heads,
+                int32_t head_dim_k, int32_t head_dim_v, void* stream);
+
+int gdn_prefill_check(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v,
+                      const float* state, const float* A_log, const gdn_bf16* a,
+                      const float* dt_bias, const gdn_bf16* b, const void* cu_seqlens,
+                      int32_t cu_seqlens_dtype, int64_t num_seqs, int64_t total_tokens,
+                      double scale, gdn_bf16* output, float* new_state,
+                      int32_t num_q_heads, int32_t num_k_heads, int32_t num_v_heads,
+                      int32_t head_dim_k, int32_t head_dim_v);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GDN_KERNEL_AMD_H */

@@ -1,0 +1,43 @@
+import os
+import sys
+
+import numpy as np
+import pytest
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+if ROOT not in sys.path:
+    sys.path.insert(0, ROOT)
+
+
+def pytest_configure(config):
+    config.addinivalue_line("markers", "gpu: needs a ROCm GPU (MI355X); run with -m gpu")
+
+
+@pytest.fixture(scope="session")
+def gpu():
+    """GPU tests never skip silently: without a visible GPU they fail."""
+    import torch
+    assert torch.cuda.is_available(), "GPU test run without a visible ROCm GPU"
+    from gdn_kernel_amd import _lib
+    _lib.load()
+    return torch.device("cuda:0")
+
+
+def close_report(got, ref, rtol, atol):
+    """(ok, message) for |got - ref| <= atol + rtol*|ref| elementwise."""
+    got = np.asarray(got, np.float64)
+    ref = np.asarray(ref, np.float64)
+    err = np.abs(got - ref)
+    bound = atol + rtol * np.abs(ref)
+    bad = ~(err <= bound)
+    if not bad.any():
+        return True, ""
+    i = np.unravel_index(np.argmax(err - bound), err.shape)
+    return False, (f"{int(bad.sum())}/{bad.size} elements outside atol={atol} rtol={rtol}; "
+                   f"worst at {tuple(int(x) for x in i)}: got {got[i]!r} ref {ref[i]!r}; "
+                   f"max abs err {err.max():.3e}")
+
+
+def assert_close(got, ref, rtol, atol, what=""):
+    ok, msg = close_report(got, ref, rtol, atol)
+    assert ok, f"{what}: {msg}"

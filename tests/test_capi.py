@@ -1,0 +1,146 @@
+"""CPU tests of the C ABI: the library loads, exports every symbol the header
+declares, and validates arguments before any device call (these run without a
+GPU; no compute entry point is called with valid arguments here)."""
+import ctypes
+import re
+import subprocess
+from pathlib import Path
+
+import pytest
+
+from gdn_kernel_amd import _lib
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "gdn_kernel_amd.h"
+
+OK, INVALID, UNSUPPORTED = _lib.GDN_OK, _lib.GDN_ERR_INVALID_ARGUMENT, _lib.GDN_ERR_UNSUPPORTED
+FAKE = 0x10000  # non-null, never dereferenced by the *_check functions
+
+
+def header_functions():
+    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
+    return sorted(set(re.findall(r"\b(gdn_[a-z_0-9]+)\s*\(", text)))
+
+
+@pytest.fixture(scope="module")
+def lib():
+    return _lib.load()
+
+
+def test_library_exports_every_header_symbol(lib):
+    names = header_functions()
+    assert {"gdn_decode", "gdn_decode_pooled", "gdn_prefill", "gdn_last_error"} <= set(names)
+    for n in names:
+        assert hasattr(lib, n), f"{n} declared in the header but not exported"
+        assert n in _lib.SIGNATURES, f"{n} has no ctypes signature in _lib.SIGNATURES"
+    out = subprocess.run(["nm", "-D", "--defined-only", str(_lib.LIB_PATH)], capture_output=True,
+                         text=True, check=True).stdout
+    exported = set(re.findall(r"\bT (gdn_\w+)", out))
+    assert set(names) <= exported
+    assert exported <= set(names), f"undeclared exports: {exported - set(names)}"
+
+
+def test_version(lib):
+    assert lib.gdn_version() >= 100
+
+
+def dec_args(**kw):
+    a = dict(q=FAKE, k=FAKE, v=FAKE, state=FAKE, A_log=FAKE, a=FAKE, dt_bias=FAKE, b=FAKE,
+             scale=0.0, output=FAKE, new_state=FAKE + (1 << 30), B=64, Hq=16, Hk=16, Hv=32,
+             dk=128, dv=128)
+    a.update(kw)
+    return [a[k] for k in ("q", "k", "v", "state", "A_log", "a", "dt_bias", "b", "scale",
+                           "output", "new_state", "B", "Hq", "Hk", "Hv", "dk", "dv")]
+
+
+def test_decode_check_accepts_valid(lib):
+    assert lib.gdn_decode_check(*dec_args()) == OK
+    assert lib.gdn_decode_check(*dec_args(state=None)) == OK            # zero initial state
+    assert lib.gdn_decode_check(*dec_args(new_state=FAKE)) == OK        # exact in-place alias
+    assert lib.gdn_decode_check(*dec_args(B=0, q=None)) == OK           # empty batch
+    assert lib.gdn_decode_check(*dec_args(Hq=4, Hk=8, Hv=32)) == OK     # distinct q/k ratios
+
+
+@pytest.mark.parametrize("kw,code,frag", [
+    (dict(B=-1), INVALID, "batch"),
+    (dict(Hv=30), INVALID, "multiple"),
+    (dict(Hq=0), INVALID, "positive"),
+    (dict(dk=64), UNSUPPORTED, "128"),
+    (dict(dv=256), UNSUPPORTED, "128"),
+    (dict(q=None), INVALID, "null"),
+    (dict(new_state=None), INVALID, "null"),
+    (dict(scale=float("nan")), INVALID, "scale"),
+    (dict(new_state=FAKE + 4096), INVALID, "overlap"),
+])
+def test_decode_rejects(lib, kw, code, frag):
+    assert lib.gdn_decode_check(*dec_args(**kw)) == code
+    assert frag in _lib.last_error()
+    # the launching entry point reports the same error without touching a device
+    assert lib.gdn_decode(*dec_args(**kw), None) == code
+
+
+def pool_args(**kw):
+    a = dict(q=FAKE, k=FAKE, v=FAKE, pool=FAKE, slots=1024, idx=FAKE, A_log=FAKE, a=FAKE,
+             dt_bias=FAKE, b=FAKE, scale=0.0, output=FAKE, B=512, Hq=16, Hk=16, Hv=32, dk=128,
+             dv=128)
+    a.update(kw)
+    return [a[k] for k in ("q", "k", "v", "pool", "slots", "idx", "A_log", "a", "dt_bias", "b",
+                           "scale", "output", "B", "Hq", "Hk", "Hv", "dk", "dv")]
+
+
+def test_pooled_check(lib):
+    assert lib.gdn_decode_pooled_check(*pool_args()) == OK
+    assert lib.gdn_decode_pooled_check(*pool_args(slots=0)) == INVALID
+    assert "pool_slots" in _lib.last_error()
+    assert lib.gdn_decode_pooled_check(*pool_args(idx=None)) == INVALID
+    assert lib.gdn_decode_pooled_check(*pool_args(pool=None)) == INVALID
+    assert lib.gdn_decode_pooled(*pool_args(Hv=7), None) == INVALID
+
+
+def pre_args(**kw):
+    a = dict(q=FAKE, k=FAKE, v=FAKE, state=FAKE, A_log=FAKE, a=FAKE, dt_bias=FAKE, b=FAKE,
+             cu=FAKE, cu_dtype=_lib.GDN_INDEX_INT32, N=32, T=32768, scale=0.0, output=FAKE,
+             new_state=FAKE + (1 << 30), Hq=16, Hk=16, Hv=32, dk=128, dv=128)
+    a.update(kw)
+    return [a[k] for k in ("q", "k", "v", "state", "A_log", "a", "dt_bias", "b", "cu",
+                           "cu_dtype", "N", "T", "scale", "output", "new_state", "Hq", "Hk", "Hv",
+                           "dk", "dv")]
+
+
+def test_prefill_check_accepts_valid(lib):
+    assert lib.gdn_prefill_check(*pre_args()) == OK
+    assert lib.gdn_prefill_check(*pre_args(cu_dtype=_lib.GDN_INDEX_INT64)) == OK
+    assert lib.gdn_prefill_check(*pre_args(state=None)) == OK
+    assert lib.gdn_prefill_check(*pre_args(N=0, cu=None)) == OK
+    assert lib.gdn_prefill_check(*pre_args(T=0, q=None, k=None, v=None, a=None, b=None,
+                                           output=None)) == OK          # only empty sequences
+
+
+@pytest.mark.parametrize("kw,code,frag", [
+    (dict(cu_dtype=2), INVALID, "cu_seqlens_dtype"),
+    (dict(N=-1), INVALID, "num_seqs"),
+    (dict(T=-5), INVALID, "total_tokens"),
+    (dict(cu=None), INVALID, "null"),
+    (dict(Hk=3), INVALID, "multiple"),
+    (dict(dk=96), UNSUPPORTED, "128"),
+    (dict(new_state=FAKE + 64), INVALID, "overlap"),
+])
+def test_prefill_rejects(lib, kw, code, frag):
+    assert lib.gdn_prefill_check(*pre_args(**kw)) == code
+    assert frag in _lib.last_error()
+    assert lib.gdn_prefill(*pre_args(**kw), None) == code
+
+
+def test_last_error_is_cleared_on_success(lib):
+    lib.gdn_decode_check(*dec_args(B=-1))
+    assert _lib.last_error()
+    assert lib.gdn_decode_check(*dec_args()) == OK
+    assert _lib.last_error() == ""
+
+
+def test_check_maps_codes_to_exceptions():
+    _lib.load().gdn_decode_check(*dec_args(dk=64))
+    with pytest.raises(ValueError, match="128"):
+        _lib.check(UNSUPPORTED)
+    with pytest.raises(_lib.GDNError):
+        _lib.check(_lib.GDN_ERR_DEVICE)

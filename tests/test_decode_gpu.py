@@ -1,0 +1,153 @@
+"""GPU parity tests of the decode kernel (through the C ABI) against the CPU oracle."""
+import numpy as np
+import pytest
+import torch
+
+from gdn_kernel_amd import binding, workloads
+from gdn_kernel_amd.workloads import Heads, to_numpy
+from oracle import gdn_oracle as O
+from tests.conftest import assert_close
+from tests.gpu_util import (OUT_ATOL, OUT_RTOL, STATE_ATOL, STATE_RTOL, host, oracle_decode,
+                            run_decode, say)
+
+pytestmark = pytest.mark.gpu
+
+
+@pytest.mark.parametrize("B", [1, 3, 8])
+@pytest.mark.parametrize("gate", ["baseline", "slow"])
+@pytest.mark.parametrize("mode", ["in_place", "separate", "null_state"])
+def test_decode_matches_oracle(gpu, B, gate, mode):
+    say(f"decode parity B={B} gate={gate} mode={mode}")
+    w = workloads.decode_inputs(B, seed=100 + B, gate=gate, with_state=mode != "null_state",
+                                state_scale=1.0 if gate == "slow" else 0.05)
+    o_ref, s_ref = oracle_decode(w)
+    out, ns = run_decode(w, gpu, in_place=mode == "in_place")
+    torch.cuda.synchronize()
+    assert_close(host(out), o_ref, OUT_RTOL, OUT_ATOL, "output")
+    assert_close(host(ns), s_ref, STATE_RTOL, STATE_ATOL, "new_state")
+
+
+@pytest.mark.parametrize("hq,hk,hv", [(8, 8, 32), (4, 16, 32), (32, 32, 32), (1, 1, 4)])
+def test_decode_head_ratios(gpu, hq, hk, hv):
+    say(f"decode heads hq={hq} hk={hk} hv={hv}")
+    w = workloads.decode_inputs(4, Heads(hq, hk, hv), seed=7, gate="slow", state_scale=0.5)
+    o_ref, s_ref = oracle_decode(w)
+    out, ns = run_decode(w, gpu, in_place=False)
+    torch.cuda.synchronize()
+    assert_close(host(out), o_ref, OUT_RTOL, OUT_ATOL, "output")
+    assert_close(host(ns), s_ref, STATE_RTOL, STATE_ATOL, "new_state")
+
+
+def test_decode_scale_argument(gpu):
+    say("decode scale 0 / None / explicit")
+    w = workloads.decode_inputs(2, seed=3)
+    o_def, _ = run_decode(w, gpu, in_place=False)
+    o_none, _ = run_decode({**w, "scale": None}, gpu, in_place=False)
+    o_zero, _ = run_decode({**w, "scale": 0.0}, gpu, in_place=False)
+    o_half, _ = run_decode({**w, "scale": 0.5}, gpu, in_place=False)
+    torch.cuda.synchronize()
+    assert torch.equal(o_def, o_none) and torch.equal(o_def, o_zero)
+    ref, _ = O.decode(*[to_numpy(w[k]) for k in ("q", "k", "v", "state", "A_log", "a",
+                                                  "dt_bias", "b")], 0.5)
+    assert_close(host(o_half), ref, OUT_RTOL, OUT_ATOL, "output scale 0.5")
+
+
+def test_decode_config1_full_size(gpu):
+    """BASELINE config 1 (B=64, heads 16/16/32, state updated in place) vs the oracle."""
+    say("decode config1 B=64 full size")
+    w = workloads.config(1)
+    o_ref, s_ref = oracle_decode(w)
+    out, ns = run_decode(w, gpu, in_place=True)
+    torch.cuda.synchronize()
+    assert_close(host(out), o_ref, OUT_RTOL, OUT_ATOL, "output")
+    assert_close(host(ns), s_ref, STATE_RTOL, STATE_ATOL, "new_state")
+
+
+def test_decode_deterministic_and_alias_safe(gpu):
+    say("decode determinism / aliasing")
+    w = workloads.decode_inputs(16, seed=5, gate="slow", state_scale=0.5)
+    o1, s1 = run_decode(w, gpu, in_place=False)
+    o2, s2 = run_decode(w, gpu, in_place=True)       # fresh device copy updated in place
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2) and torch.equal(s1, s2)
+
+
+def test_decode_empty_batch(gpu):
+    say("decode B=0")
+    w = workloads.decode_inputs(0, seed=1)
+    out, ns = run_decode(w, gpu, in_place=True)
+    torch.cuda.synchronize()
+    assert out.numel() == 0
+
+
+@pytest.mark.parametrize("gate", ["baseline", "slow"])
+def test_decode_pooled_matches_oracle(gpu, gate):
+    say(f"decode pooled small gate={gate}")
+    slots, B = 40, 12
+    w = workloads.decode_inputs(B, seed=9, gate=gate, pool_slots=slots,
+                                state_scale=1.0 if gate == "slow" else 0.05)
+    idx = w["state_indices"].clone()
+    idx[3] = -1                      # padding row
+    idx[7] = slots + 5               # out of range: treated as padding
+    d = {k: (v.to(gpu) if isinstance(v, torch.Tensor) else v) for k, v in w.items()}
+    pool = d["state"].clone()
+    out = torch.full_like(d["v"], float("nan"))
+    binding.decode_pooled_kernel(d["q"], d["k"], d["v"], pool, d["A_log"], d["a"], d["dt_bias"],
+                                 d["b"], d["scale"], out, idx.to(gpu))
+    torch.cuda.synchronize()
+    o_ref, pool_ref = O.decode_pooled(*[to_numpy(w[k]) for k in ("q", "k", "v", "state")],
+                                      idx.numpy(), *[to_numpy(w[k]) for k in
+                                                     ("A_log", "a", "dt_bias", "b")], w["scale"])
+    assert_close(host(out), o_ref, OUT_RTOL, OUT_ATOL, "output")
+    assert not host(out)[[3, 7]].any()
+    assert_close(host(pool), pool_ref, STATE_RTOL, STATE_ATOL, "pool")
+    used = set(int(i) for i in idx.tolist() if 0 <= i < slots)
+    untouched = [s for s in range(slots) if s not in used]
+    assert torch.equal(pool[untouched], d["state"][untouched]), "untouched slots changed"
+
+
+def test_decode_pooled_config2_full_size(gpu):
+    """BASELINE config 2 (B=512 over a 1024-slot pool): untouched slots are bit-identical;
+    touched slots equal the contiguous decode kernel on the gathered states; a sample of rows
+    matches the oracle."""
+    say("decode pooled config2 full size")
+    w = workloads.decode_inputs(512, seed=2, pool_slots=1024, device=gpu)
+    idx = w["state_indices"]
+    pool = w["state"].clone()
+    out = torch.empty_like(w["v"])
+    binding.decode_pooled_kernel(w["q"], w["k"], w["v"], pool, w["A_log"], w["a"], w["dt_bias"],
+                                 w["b"], w["scale"], out, idx)
+    gathered = w["state"][idx.long()]
+    out2 = torch.empty_like(w["v"])
+    binding.decode_kernel(w["q"], w["k"], w["v"], gathered, w["A_log"], w["a"], w["dt_bias"],
+                          w["b"], w["scale"], out2, gathered)
+    torch.cuda.synchronize()
+    mask = torch.ones(1024, dtype=torch.bool, device=gpu)
+    mask[idx.long()] = False
+    assert torch.equal(pool[mask], w["state"][mask])
+    assert torch.equal(out, out2)
+    assert torch.equal(pool[idx.long()], gathered)
+    sample = [0, 1, 255, 511]
+    sub = {k: (w[k][sample] if k in ("q", "k", "v", "a", "b") else w[k])
+           for k in ("q", "k", "v", "a", "b", "A_log", "dt_bias", "scale")}
+    sub["state"] = w["state"][idx.long()[sample]]
+    o_ref, s_ref = oracle_decode(sub)
+    assert_close(host(out[sample]), o_ref, OUT_RTOL, OUT_ATOL, "output sample")
+    assert_close(host(pool[idx.long()[sample]]), s_ref, STATE_RTOL, STATE_ATOL, "state sample")
+
+
+def test_decode_golden_fixture(gpu):
+    say("decode golden fixture")
+    fx = np.load(__import__("tests.golden", fromlist=["x"]).path("decode_small.npz"))
+    t = lambda a, dt: torch.from_numpy(a).to(gpu).view(dt) if a.dtype == np.uint16 \
+        else torch.from_numpy(a).to(gpu)
+    q, k, v = (t(fx[n], torch.bfloat16) for n in ("q", "k", "v"))
+    a, b = t(fx["a"], torch.bfloat16), t(fx["b"], torch.bfloat16)
+    state = torch.from_numpy(O.bits_to_f32(fx["state"])).to(gpu)
+    out = torch.empty_like(v)
+    ns = torch.empty_like(state)
+    binding.decode_kernel(q, k, v, state, t(fx["A_log"], None), a, t(fx["dt_bias"], None), b,
+                          float(fx["scale"]), out, ns)
+    torch.cuda.synchronize()
+    assert_close(host(out), fx["out_ref"], OUT_RTOL, OUT_ATOL, "output")
+    assert_close(host(ns), fx["state_ref"], STATE_RTOL, STATE_ATOL, "new_state")

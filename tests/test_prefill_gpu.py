@@ -1,0 +1,179 @@
+"""GPU parity tests of the varlen chunked prefill kernel (through the C ABI)
+against the CPU oracle, plus size-independent properties at full size."""
+import numpy as np
+import pytest
+import torch
+
+from gdn_kernel_amd import binding, workloads
+from gdn_kernel_amd.workloads import Heads, to_numpy
+from oracle import gdn_oracle as O
+from tests.conftest import assert_close
+from tests.gpu_util import (OUT_ATOL, OUT_RTOL, STATE_ATOL, STATE_RTOL, host, oracle_prefill,
+                            run_decode, run_prefill, say)
+
+pytestmark = pytest.mark.gpu
+
+CASES = {
+    "one_chunk": [64],
+    "one_token": [1],
+    "short": [63],
+    "partial": [65],
+    "two_seqs": [130, 7],
+    "ragged_empty": [0, 5, 64, 0, 200],
+    "long": [300],
+}
+
+
+@pytest.mark.parametrize("case", list(CASES))
+@pytest.mark.parametrize("gate", ["baseline", "slow"])
+def test_prefill_matches_oracle(gpu, case, gate):
+    lens = CASES[case]
+    say(f"prefill parity case={case} lens={lens} gate={gate}")
+    p = workloads.prefill_inputs(lens, seed=len(lens) * 7 + sum(lens), gate=gate,
+                                 state_scale=0.5 if gate == "slow" else 0.05)
+    o_ref, s_ref = oracle_prefill(p)
+    out, ns = run_prefill(p, gpu)
+    torch.cuda.synchronize()
+    assert_close(host(out), o_ref, OUT_RTOL, OUT_ATOL, "output")
+    assert_close(host(ns), s_ref, STATE_RTOL, STATE_ATOL, "new_state")
+
+
+@pytest.mark.parametrize("cu_dtype", [torch.int32, torch.int64])
+def test_prefill_null_state_and_cu_dtypes(gpu, cu_dtype):
+    say(f"prefill null state cu={cu_dtype}")
+    p = workloads.prefill_inputs([70, 3, 0], seed=11, gate="slow", with_state=False,
+                                 cu_dtype=cu_dtype)
+    o_ref, s_ref = oracle_prefill(p)
+    out, ns = run_prefill(p, gpu)
+    torch.cuda.synchronize()
+    assert_close(host(out), o_ref, OUT_RTOL, OUT_ATOL, "output")
+    assert_close(host(ns), s_ref, STATE_RTOL, STATE_ATOL, "new_state")
+    assert not host(ns)[2].any()                      # empty sequence, zero initial state
+
+
+def test_prefill_in_place(gpu):
+    say("prefill in place")
+    p = workloads.prefill_inputs([100, 0, 20], seed=12, gate="slow", state_scale=0.5)
+    o1, s1 = run_prefill(p, gpu, in_place=False)
+    o2, s2 = run_prefill(p, gpu, in_place=True)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2) and torch.equal(s1, s2)
+
+
+@pytest.mark.parametrize("hq,hk,hv", [(8, 8, 32), (32, 32, 32), (2, 4, 8)])
+def test_prefill_head_ratios(gpu, hq, hk, hv):
+    say(f"prefill heads hq={hq} hk={hk} hv={hv}")
+    p = workloads.prefill_inputs([90, 17], Heads(hq, hk, hv), seed=13, gate="slow",
+                                 state_scale=0.5)
+    o_ref, s_ref = oracle_prefill(p)
+    out, ns = run_prefill(p, gpu)
+    torch.cuda.synchronize()
+    assert_close(host(out), o_ref, OUT_RTOL, OUT_ATOL, "output")
+    assert_close(host(ns), s_ref, STATE_RTOL, STATE_ATOL, "new_state")
+
+
+def test_prefill_sequential_definition(gpu):
+    """Against the token-by-token definition directly (not only the chunk form)."""
+    say("prefill vs sequential definition")
+    p = workloads.prefill_inputs([150, 40], Heads(4, 4, 8), seed=14, gate="slow",
+                                 state_scale=0.5)
+    o_ref, s_ref = oracle_prefill(p, chunked=False)
+    out, ns = run_prefill(p, gpu)
+    torch.cuda.synchronize()
+    assert_close(host(out), o_ref, OUT_RTOL, OUT_ATOL, "output")
+    assert_close(host(ns), s_ref, STATE_RTOL, STATE_ATOL, "new_state")
+
+
+def test_prefill_T1_equals_decode_kernel(gpu):
+    say("prefill T=1 vs decode kernel")
+    p = workloads.prefill_inputs([1] * 5, seed=15, gate="slow", state_scale=0.5)
+    out, ns = run_prefill(p, gpu)
+    w = {k: p[k][:, None] if k in ("q", "k", "v", "a", "b") else p[k]
+         for k in ("q", "k", "v", "a", "b", "A_log", "dt_bias", "state", "scale")}
+    o2, s2 = run_decode(w, gpu, in_place=False)
+    torch.cuda.synchronize()
+    assert_close(host(out), host(o2[:, 0]), OUT_RTOL, OUT_ATOL, "output")
+    assert_close(host(ns), host(s2), STATE_RTOL, STATE_ATOL, "state")
+
+
+def test_prefill_golden_fixture(gpu):
+    say("prefill golden fixture")
+    from tests.golden import path
+    fx = np.load(path("prefill_small.npz"))
+    bf = lambda n: torch.from_numpy(fx[n]).to(gpu).view(torch.bfloat16)
+    state = torch.from_numpy(O.bits_to_f32(fx["state"])).to(gpu)
+    out = torch.empty((fx["v"].shape[0], fx["v"].shape[1], 128), dtype=torch.bfloat16, device=gpu)
+    ns = torch.empty_like(state)
+    binding.prefill_kernel(bf("q"), bf("k"), bf("v"), state, torch.from_numpy(fx["A_log"]).to(gpu),
+                           bf("a"), torch.from_numpy(fx["dt_bias"]).to(gpu), bf("b"),
+                           torch.from_numpy(fx["cu_seqlens"]).to(gpu), float(fx["scale"]), out, ns)
+    torch.cuda.synchronize()
+    assert_close(host(out), fx["out_ref"], OUT_RTOL, OUT_ATOL, "output")
+    assert_close(host(ns), fx["state_ref"], STATE_RTOL, STATE_ATOL, "new_state")
+
+
+def _split_run(p, cut, gpu):
+    """Run a single sequence in two calls, handing the state over at ``cut``."""
+    d = {k: (v.to(gpu) if isinstance(v, torch.Tensor) else v) for k, v in p.items()}
+    T = d["q"].shape[0]
+    out = torch.empty((T, d["v"].shape[1], 128), dtype=torch.bfloat16, device=gpu)
+    st = d["state"].clone() if d["state"] is not None else torch.zeros(
+        (1, d["v"].shape[1], 128, 128), device=gpu)
+    for s, e in ((0, cut), (cut, T)):
+        cu = torch.tensor([0, e - s], dtype=torch.int32, device=gpu)
+        binding.prefill_kernel(d["q"][s:e], d["k"][s:e], d["v"][s:e], st, d["A_log"], d["a"][s:e],
+                               d["dt_bias"], d["b"][s:e], cu, d["scale"], out[s:e], st)
+    return out, st
+
+
+def test_prefill_config3_full_size(gpu):
+    """BASELINE config 3 (T=4096, one sequence, zero initial state): compared with the
+    oracle on the first 256 tokens (a separate call), and with itself split in two calls
+    at a chunk boundary and off a chunk boundary (state hand-off)."""
+    say("prefill config3 full size")
+    p = workloads.config(3)
+    out, ns = run_prefill(p, gpu)
+    head = {k: (p[k][:256] if k in ("q", "k", "v", "a", "b") else p[k])
+            for k in ("q", "k", "v", "a", "b", "A_log", "dt_bias", "state", "scale")}
+    head["cu_seqlens"] = torch.tensor([0, 256], dtype=torch.int32)
+    o_ref, _ = oracle_prefill(head)
+    torch.cuda.synchronize()
+    assert_close(host(out[:256]), o_ref, OUT_RTOL, OUT_ATOL, "output[:256]")
+    for cut in (2048, 1000):
+        o2, s2 = _split_run(p, cut, gpu)
+        torch.cuda.synchronize()
+        assert_close(host(o2), host(out), OUT_RTOL, OUT_ATOL, f"split@{cut} output")
+        assert_close(host(s2), host(ns), STATE_RTOL, STATE_ATOL, f"split@{cut} state")
+
+
+def test_prefill_config4_full_size(gpu):
+    """BASELINE config 4 (32 sequences, 32768 tokens, int32 cu_seqlens, random initial
+    states): every sequence's final state and the outputs of its first tokens against
+    the oracle, on the shortest sequences in full."""
+    say("prefill config4 full size")
+    p = workloads.config(4)
+    lens = p["lengths"]
+    assert min(lens) < 64 and sum(lens) == 32768
+    out, ns = run_prefill(p, gpu)
+    torch.cuda.synchronize()
+    cu = p["cu_seqlens"].tolist()
+    order = np.argsort(lens)
+    for i in list(order[:4]) + [int(order[len(order) // 2])]:
+        s, e = cu[i], cu[i + 1]
+        sub = {k: (p[k][s:e] if k in ("q", "k", "v", "a", "b") else p[k])
+               for k in ("q", "k", "v", "a", "b", "A_log", "dt_bias", "scale")}
+        sub["state"] = p["state"][i:i + 1]
+        sub["cu_seqlens"] = torch.tensor([0, e - s], dtype=torch.int32)
+        o_ref, s_ref = oracle_prefill(sub)
+        assert_close(host(out[s:e]), o_ref, OUT_RTOL, OUT_ATOL, f"seq {i} (len {e - s}) output")
+        assert_close(host(ns[i]), s_ref[0], STATE_RTOL, STATE_ATOL, f"seq {i} state")
+    # varlen packing: each sequence run on its own gives the same result
+    for i in (int(order[-1]), int(order[0])):
+        s, e = cu[i], cu[i + 1]
+        sub = {k: (p[k][s:e] if k in ("q", "k", "v", "a", "b") else p[k])
+               for k in ("q", "k", "v", "a", "b", "A_log", "dt_bias", "scale")}
+        sub["state"] = p["state"][i:i + 1]
+        sub["cu_seqlens"] = torch.tensor([0, e - s], dtype=torch.int32)
+        o1, s1 = run_prefill(sub, gpu)
+        torch.cuda.synchronize()
+        assert torch.equal(o1, out[s:e]) and torch.equal(s1[0], ns[i]), f"seq {i} packed != alone"
