@@ -1,0 +1,231 @@
+#!/usr/bin/env python3
+"""Benchmark of the MI355X GDN hot path; prints ONE JSON line.
+
+Headline (``value``): GDN decode at B=64 (heads 16/16/32, dk=dv=128, fp32 state
+[64,32,128,128] updated in place) as algorithmic HBM GB/s:
+  bytes/step = 2*B*Hv*dv*dk*4 (state in + out) + B*(2*Hq*dk*2 + 2*Hv*dv*2 + 2*Hv*2)
+               (q, k, v, output, a, b) + 2*Hv*4 (A_log, dt_bias) = 270,016,768 B.
+Inputs are resident in HBM before the timed region.  To keep the 256 MB
+Infinity Cache from serving the state, steps rotate over 4 independent state
+buffers (537 MB).
+
+Also reported on the same line: pooled decode (B=512 over a 1024-slot pool),
+chunked prefill tokens/s on the 32-sequence / 32768-token varlen batch and on
+the single 4096-token sequence (with MFMA-roofline fractions computed from the
+algorithmic 180,224 FLOP per token and v-head), and the CPU baseline (the numpy
+oracle, the reference decode definition restated, timed on the host).
+
+Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only decode|prefill]
+       [--no-cpu] [--cpu-seconds S]
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import platform
+import sys
+import time
+
+import numpy as np
+
+HBM_PEAK_GBS = 8000.0          # MI355X HBM3E, GB/s
+MFMA_BF16_PEAK_TFS = 2516.6    # MI355X dense bf16 MFMA, TFLOP/s
+PREFILL_FLOP_PER_TOKEN_HEAD = 180224   # 2*(5*C*d + 3*dk*dv), C=64, d=128
+HQ, HK, HV, D = 16, 16, 32, 128
+
+
+def decode_bytes(B, slots_idx=False):
+    b = 2 * B * HV * D * D * 4 + B * (2 * HQ * D * 2 + 2 * HV * D * 2 + 2 * HV * 2) + 2 * HV * 4
+    if slots_idx:
+        b += 4 * B
+    return b
+
+
+def parse():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--only", choices=["decode", "prefill", "all"], default="all")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    return ap.parse_args()
+
+
+def timed_launches(fn, steps, warmup, torch):
+    """Warm up, then time exactly ``steps`` launches.  Returns (wall seconds for
+    the steps between two synchronisations, mean per-launch GPU ms from HIP events
+    recorded on the launch stream)."""
+    for i in range(warmup):
+        fn(i)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+          for _ in range(steps)]
+    torch.cuda.synchronize()
+    t0 = time.perf_counter()
+    for i in range(steps):
+        ev[i][0].record(stream)
+        fn(warmup + i)
+        ev[i][1].record(stream)
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - t0
+    per = [a.elapsed_time(b) for a, b in ev]
+    return wall, float(np.mean(per)), float(np.median(per))
+
+
+def bench_decode(args, torch, binding, workloads):
+    dev = torch.device("cuda:0")
+    B = 64
+    nbuf = 4
+    w = workloads.decode_inputs(B, seed=1, device=dev)
+    states = [w["state"]] + [w["state"].clone() for _ in range(nbuf - 1)]
+    out = torch.empty_like(w["v"])
+
+    def step(i):
+        st = states[i % nbuf]
+        binding.decode_kernel(w["q"], w["k"], w["v"], st, w["A_log"], w["a"], w["dt_bias"],
+                              w["b"], w["scale"], out, st)
+
+    wall, ev_mean, ev_med = timed_launches(step, args.steps, args.warmup, torch)
+    nbytes = decode_bytes(B)
+    return dict(bytes=nbytes, wall=wall, ev_mean_ms=ev_mean, ev_med_ms=ev_med)
+
+
+def bench_pooled(args, torch, binding, workloads):
+    dev = torch.device("cuda:0")
+    w = workloads.decode_inputs(512, seed=2, device=dev, pool_slots=1024)
+    out = torch.empty_like(w["v"])
+
+    def step(i):
+        binding.decode_pooled_kernel(w["q"], w["k"], w["v"], w["state"], w["A_log"], w["a"],
+                                     w["dt_bias"], w["b"], w["scale"], out, w["state_indices"])
+
+    steps = max(5, args.steps // 2)
+    wall, ev_mean, ev_med = timed_launches(step, steps, min(args.warmup, 3), torch)
+    nbytes = decode_bytes(512, slots_idx=True)
+    return dict(us=ev_mean * 1e3, gbs=nbytes / (ev_mean * 1e-3) / 1e9,
+                frac=nbytes / (ev_mean * 1e-3) / 1e9 / HBM_PEAK_GBS, bytes=nbytes)
+
+
+def bench_prefill(args, torch, binding, workloads, cfg):
+    dev = torch.device("cuda:0")
+    p = workloads.config(cfg, device=dev)
+    T = p["q"].shape[0]
+    N = p["cu_seqlens"].numel() - 1
+    out = torch.empty((T, HV, D), dtype=torch.bfloat16, device=dev)
+    ns = torch.empty((N, HV, D, D), dtype=torch.float32, device=dev)
+
+    def step(i):
+        binding.prefill_kernel(p["q"], p["k"], p["v"], p["state"], p["A_log"], p["a"],
+                               p["dt_bias"], p["b"], p["cu_seqlens"], p["scale"], out, ns)
+
+    steps = max(3, args.steps // 5)
+    wall, ev_mean, ev_med = timed_launches(step, steps, min(args.warmup, 2), torch)
+    flop = HV * T * PREFILL_FLOP_PER_TOKEN_HEAD
+    tfs = flop / (ev_mean * 1e-3) / 1e12
+    return dict(tokens=T, seqs=N, us=ev_mean * 1e3, tokens_per_s=T / (ev_mean * 1e-3),
+                tflops=tfs, mfma_frac=tfs / MFMA_BF16_PEAK_TFS, flop=flop,
+                lengths=p["lengths"] if cfg == 4 else None)
+
+
+def cpu_baseline(seconds, workloads):
+    """The oracle's decode (design.md:166-226 restated in numpy, fp32 arithmetic like the
+    reference's .float() path) on BASELINE config 0 (B=1), single-threaded."""
+    from threadpoolctl import threadpool_limits
+    from oracle import gdn_oracle as O
+    w = workloads.config(0)
+    a = [workloads.to_numpy(w[k]).astype(np.float32) for k in
+         ("q", "k", "v", "state", "A_log", "a", "dt_bias", "b")]
+    times = []
+    with threadpool_limits(limits=1):
+        O.decode(*a, w["scale"], dtype=np.float32)
+        t_end = time.perf_counter() + seconds
+        while time.perf_counter() < t_end or len(times) < 5:
+            t0 = time.perf_counter()
+            O.decode(*a, w["scale"], dtype=np.float32)
+            times.append(time.perf_counter() - t0)
+    med = float(np.median(times))
+    nbytes = decode_bytes(1)
+    cpu = platform.processor() or platform.machine()
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    cpu = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    return {"value": nbytes / med / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
+            "us_per_step": med * 1e6,
+            "sample": (f"oracle decode (numpy fp32, 1 thread) on config 0: B=1, 32 v-heads, "
+                       f"{nbytes} algorithmic bytes/step; median of {len(times)} steps over "
+                       f"~{seconds:.0f} s"),
+            "cpu_model": cpu}
+
+
+def load_traffic():
+    """HBM bytes per decode launch measured with rocprofv3 PMC counters, if a
+    measurement has been recorded under profiles/."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                        "decode_b64_traffic.json")
+    try:
+        with open(path) as f:
+            return json.load(f).get("traffic_bytes")
+    except (OSError, ValueError):
+        return None
+
+
+def main():
+    args = parse()
+    if args.gpus != 1:
+        print(f"bench.py: this build runs on one GPU only (asked for --gpus {args.gpus}); "
+              "the decode and prefill paths shard with no exchange and are measured on one "
+              "GPU's share", file=sys.stderr)
+        sys.exit(2)
+    import torch
+    from gdn_kernel_amd import binding, workloads, _lib
+    _lib.load()
+    assert torch.cuda.is_available(), "no ROCm GPU visible"
+
+    res = {"metric": "GDN decode µs + HBM GB/s at B=64; prefill tokens/s (32k varlen), 1 GPU",
+           "value": None, "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
+           "warmup": args.warmup, "ms_per_step": None, "higher_is_better": True,
+           "scaling": "weak", "vs_baseline": None, "dtype": "fp32", "data": "synthetic",
+           "config": {"workload": "GDN decode, B=64, one token, Hq=Hk=16, Hv=32, dk=dv=128, "
+                                  "bf16 q/k/v/a/b, fp32 state [64,32,128,128] updated in place "
+                                  "(4 rotating state buffers, cold Infinity Cache)",
+                      "batch": 64, "heads": [HQ, HK, HV], "head_dim": D}}
+    if args.only in ("decode", "all"):
+        d = bench_decode(args, torch, binding, workloads)
+        gbs_wall = d["bytes"] * args.steps / d["wall"] / 1e9
+        gbs_kernel = d["bytes"] / (d["ev_mean_ms"] * 1e-3) / 1e9
+        res["value"] = round(gbs_wall, 1)
+        res["ms_per_step"] = round(d["wall"] / args.steps * 1e3, 5)
+        res["decode_us"] = round(d["ev_mean_ms"] * 1e3, 2)
+        res["decode_us_median"] = round(d["ev_med_ms"] * 1e3, 2)
+        res["roofline"] = {"bound": "hbm", "achieved": round(gbs_kernel, 1),
+                           "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                           "frac": round(gbs_kernel / HBM_PEAK_GBS, 4),
+                           "traffic": load_traffic(),
+                           "kernel": "gdn_decode_kernel", "bytes_per_launch": d["bytes"]}
+        pooled = bench_pooled(args, torch, binding, workloads)
+        res["decode_pooled_b512"] = {k: (round(v, 4) if isinstance(v, float) else v)
+                                     for k, v in pooled.items()}
+    if args.only in ("prefill", "all"):
+        for cfg, key in ((4, "prefill_varlen_32k"), (3, "prefill_t4096")):
+            pr = bench_prefill(args, torch, binding, workloads, cfg)
+            res[key] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in pr.items()}
+        if res["value"] is None:
+            res["value"] = round(res["prefill_varlen_32k"]["tokens_per_s"], 1)
+            res["unit"] = "tokens/s"
+            res["ms_per_step"] = round(res["prefill_varlen_32k"]["us"] / 1e3, 5)
+    if not args.no_cpu:
+        res["cpu_baseline"] = cpu_baseline(args.cpu_seconds, workloads)
+    print(json.dumps(res), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -16,18 +16,23 @@ __device__ __forceinline__ float bf16_to_f32(uint16_t h) {
   return __uint_as_float(uint32_t(h) << 16);
 }
 
-// Round-to-nearest-even float -> bf16 bits; NaN stays NaN (quiet bit set).
+typedef __bf16 gdn_bf16x2_t __attribute__((ext_vector_type(2)));
+typedef float gdn_f32x2_t __attribute__((ext_vector_type(2)));
+
+// Round-to-nearest-even float -> bf16 bits (gfx950 v_cvt_pk_bf16_f32; NaN stays NaN).
 __device__ __forceinline__ uint16_t f32_to_bf16(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return uint16_t((u >> 16) | 0x40u);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return uint16_t(u >> 16);
+  return __builtin_bit_cast(uint16_t, static_cast<__bf16>(f));
 }
 
-// Two bf16 values packed into one dword (lo element in the low half).
+// Two bf16 values packed into one dword (lo element in the low half), one instruction.
 __device__ __forceinline__ uint32_t pack_bf16x2(float lo, float hi) {
-  return uint32_t(f32_to_bf16(lo)) | (uint32_t(f32_to_bf16(hi)) << 16);
+  const gdn_f32x2_t v = {lo, hi};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(v, gdn_bf16x2_t));
 }
+
+// The two floats a packed bf16 pair represents.
+__device__ __forceinline__ float bf16lo_f32(uint32_t w) { return __uint_as_float(w << 16); }
+__device__ __forceinline__ float bf16hi_f32(uint32_t w) { return __uint_as_float(w & 0xffff0000u); }
 
 // softplus with the torch default threshold: x > 20 -> x.
 __device__ __forceinline__ float softplus20(float x) {

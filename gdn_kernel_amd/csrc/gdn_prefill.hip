@@ -49,15 +49,24 @@ constexpr int NTHREADS = 256;
 struct __align__(16) PrefillSmem {
   uint16_t K[C * KSTR];     // K chunk [c][perm(k)]
   uint16_t Q[C * KSTR];     // Q chunk [c][perm(k)]
+  uint16_t V[C * KSTR];     // V chunk [c][v]
+  uint16_t O[C * KSTR];     // output tile [c][v], staged for 16-byte stores
   uint16_t Kt[D * TSTR];    // K^T     [k][perm(c)]
   uint16_t Th[C * TSTR];    // T~ hi   [c][perm(j)]
   uint16_t Tl[C * TSTR];    // T~ lo   [c][perm(j)]
   uint16_t P[C * TSTR];     // P (bf16)[c][perm(j)]
   float N[C * FSTR];        // N (fp32, strictly lower)
   float X[C * FSTR];        // T~ (fp32) and solve scratch in its upper blocks
-  float gam[C];
-  float bet[C];
+  float gam[C];             // gamma_c (inclusive cumsum of the log gates)
+  float bet[C];             // beta_c
+  float eg[C];              // e^{gamma_c}
+  float dd[C];              // e^{gamma_last - gamma_c}
 };
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+// e^{x} for x <= 0 via the hardware exp2 (v_exp_f32).
+__device__ __forceinline__ float exp_le0(float x) { return __builtin_amdgcn_exp2f(x * kLog2e); }
 
 __device__ __forceinline__ f32x4 mfma(const uint4& a, const uint4& b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
@@ -76,20 +85,20 @@ __device__ __forceinline__ uint4 frag(const uint16_t* tile, int stride, int row0
   return *reinterpret_cast<const uint4*>(tile + (row0 + (lane & 15)) * stride + 32 * ks + 8 * (lane >> 4));
 }
 
-__device__ __forceinline__ float bf16_hi(float x) { return bf16_to_f32(f32_to_bf16(x)); }
-
 // B fragment (bf16 hi parts) from two accumulator tiles stacked along the
 // contraction dim.
 __device__ __forceinline__ uint4 pack_hi(const f32x4& t0, const f32x4& t1) {
   return uint4{pack_bf16x2(t0[0], t0[1]), pack_bf16x2(t0[2], t0[3]), pack_bf16x2(t1[0], t1[1]),
                pack_bf16x2(t1[2], t1[3])};
 }
-// The bf16 lo parts: x - hi(x), itself rounded to bf16.
-__device__ __forceinline__ uint4 pack_lo(const f32x4& t0, const f32x4& t1) {
-  return uint4{pack_bf16x2(t0[0] - bf16_hi(t0[0]), t0[1] - bf16_hi(t0[1])),
-               pack_bf16x2(t0[2] - bf16_hi(t0[2]), t0[3] - bf16_hi(t0[3])),
-               pack_bf16x2(t1[0] - bf16_hi(t1[0]), t1[1] - bf16_hi(t1[1])),
-               pack_bf16x2(t1[2] - bf16_hi(t1[2]), t1[3] - bf16_hi(t1[3]))};
+// bf16 lo parts x - hi(x) (exact in fp32), rounded to bf16, given the hi words.
+__device__ __forceinline__ uint32_t lo_word(float a, float b, uint32_t hi) {
+  return pack_bf16x2(a - bf16lo_f32(hi), b - bf16hi_f32(hi));
+}
+__device__ __forceinline__ void split_pack(const f32x4& t0, const f32x4& t1, uint4& hi, uint4& lo) {
+  hi = pack_hi(t0, t1);
+  lo = uint4{lo_word(t0[0], t0[1], hi.x), lo_word(t0[2], t0[3], hi.y), lo_word(t1[0], t1[1], hi.z),
+             lo_word(t1[2], t1[3], hi.w)};
 }
 
 __device__ __forceinline__ int64_t load_cu(const void* cu, int is64, int i) {
@@ -229,37 +238,44 @@ __global__ __launch_bounds__(NTHREADS) void gdn_prefill_kernel(PrefillArgs p) {
   }
 
   if (s1 > s0) {
+    // P's strictly-upper 16x16 blocks are read by the P v_new product but never
+    // written per chunk: zero the whole tile once (the first barrier of the chunk
+    // loop orders this before any read).
+    for (int e = tid; e < C * TSTR / 8; e += NTHREADS)
+      reinterpret_cast<uint4*>(sm.P)[e] = uint4{0u, 0u, 0u, 0u};
     const float A_log = p.A_log[h];
     const float dt_bias = p.dt_bias[h];
-    const int64_t qk_stride = int64_t(p.Hq) * D;  // token stride of q
-    const int64_t kk_stride = int64_t(p.Hk) * D;  // token stride of k
-    const int64_t vv_stride = int64_t(p.Hv) * D;  // token stride of v / out
+    const int64_t q_stride = int64_t(p.Hq) * D;   // token stride of q
+    const int64_t k_stride = int64_t(p.Hk) * D;   // token stride of k
+    const int64_t v_stride = int64_t(p.Hv) * D;   // token stride of v / out
 
     for (int64_t cs = s0; cs < s1; cs += C) {
       const int clen = int(s1 - cs < C ? s1 - cs : C);
-      __syncthreads();  // previous chunk's LDS reads are done
+      __syncthreads();  // the previous chunk's LDS reads are done
 
-      // ---- stage K, Q (permuted rows) and K^T; gates ------------------------
+      // ---- stage K, Q, V and K^T; wave w loads column segment 4*it + w ------
+      // of all 64 tokens, so the K^T writes of one instruction fill one row.
 #pragma unroll
-      for (int it = 0; it < (C * D / 8) / NTHREADS; ++it) {
-        const int seg = tid + it * NTHREADS;  // 16-byte segment index
-        const int c = seg >> 4, s = seg & 15;
-        uint4 kv = uint4{0u, 0u, 0u, 0u}, qv = uint4{0u, 0u, 0u, 0u};
+      for (int it = 0; it < 4; ++it) {
+        const int c = lane, sg = 4 * it + wave;    // token, 8-column segment
+        uint4 kv = uint4{0u, 0u, 0u, 0u}, qv = kv, vv = kv;
         if (c < clen) {
-          kv = *reinterpret_cast<const uint4*>(p.k + (cs + c) * kk_stride + int64_t(hk) * D + 8 * s);
-          qv = *reinterpret_cast<const uint4*>(p.q + (cs + c) * qk_stride + int64_t(hq) * D + 8 * s);
+          kv = *reinterpret_cast<const uint4*>(p.k + (cs + c) * k_stride + int64_t(hk) * D + 8 * sg);
+          qv = *reinterpret_cast<const uint4*>(p.q + (cs + c) * q_stride + int64_t(hq) * D + 8 * sg);
+          vv = *reinterpret_cast<const uint4*>(p.v + (cs + c) * v_stride + int64_t(h) * D + 8 * sg);
         }
-        const int col0 = (8 * s) & ~31, r0 = (8 * s) & 31;
+        const int col0 = (8 * sg) & ~31, r0 = (8 * sg) & 31;
         const int pa = col0 + perm32(r0), pb = col0 + perm32(r0 + 4);
         *reinterpret_cast<uint2*>(sm.K + c * KSTR + pa) = uint2{kv.x, kv.y};
         *reinterpret_cast<uint2*>(sm.K + c * KSTR + pb) = uint2{kv.z, kv.w};
         *reinterpret_cast<uint2*>(sm.Q + c * KSTR + pa) = uint2{qv.x, qv.y};
         *reinterpret_cast<uint2*>(sm.Q + c * KSTR + pb) = uint2{qv.z, qv.w};
+        *reinterpret_cast<uint4*>(sm.V + c * KSTR + 8 * sg) = vv;
         const int pc = perm(c);
         const uint32_t w[4] = {kv.x, kv.y, kv.z, kv.w};
 #pragma unroll
         for (int e = 0; e < 8; ++e)
-          sm.Kt[(8 * s + e) * TSTR + pc] = uint16_t(e & 1 ? (w[e >> 1] >> 16) : (w[e >> 1] & 0xffffu));
+          sm.Kt[(8 * sg + e) * TSTR + pc] = uint16_t(e & 1 ? (w[e >> 1] >> 16) : (w[e >> 1] & 0xffffu));
       }
       if (wave == 0) {
         float lg = 0.f, bt = 0.f;
@@ -268,8 +284,12 @@ __global__ __launch_bounds__(NTHREADS) void gdn_prefill_kernel(PrefillArgs p) {
           lg = log_gate(A_log, bf16_to_f32(p.a[idx]), dt_bias);
           bt = sigmoidf_(bf16_to_f32(p.b[idx]));
         }
-        sm.gam[lane] = wave_inclusive_scan(lg, lane);
+        const float gm = wave_inclusive_scan(lg, lane);
+        const float glast = readlane_f(gm, clen - 1);
+        sm.gam[lane] = gm;
         sm.bet[lane] = bt;
+        sm.eg[lane] = expf(gm);
+        sm.dd[lane] = expf(glast - gm);
       }
       __syncthreads();
 
@@ -292,7 +312,7 @@ __global__ __launch_bounds__(NTHREADS) void gdn_prefill_kernel(PrefillArgs p) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int r = 16 * I + 4 * g + i;
-            sm.N[r * FSTR + c] = r > c ? sm.bet[r] * expf(sm.gam[r] - gc) * acc[i] : 0.f;
+            sm.N[r * FSTR + c] = r > c ? sm.bet[r] * exp_le0(sm.gam[r] - gc) * acc[i] : 0.f;
           }
         } else {
 #pragma unroll
@@ -305,7 +325,7 @@ __global__ __launch_bounds__(NTHREADS) void gdn_prefill_kernel(PrefillArgs p) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) {
             const int j = 16 * J + 4 * g + i;
-            pv[i] = j <= c ? expf(gc - sm.gam[j]) * acc[i] : 0.f;
+            pv[i] = j <= c ? exp_le0(gc - sm.gam[j]) * acc[i] : 0.f;
           }
           *reinterpret_cast<uint2*>(sm.P + c * TSTR + perm(16 * J + 4 * g)) =
               uint2{pack_bf16x2(pv[0], pv[1]), pack_bf16x2(pv[2], pv[3])};
@@ -319,18 +339,16 @@ __global__ __launch_bounds__(NTHREADS) void gdn_prefill_kernel(PrefillArgs p) {
       for (int it = 0; it < 4; ++it) {
         const int grp = tid + it * NTHREADS;   // 1024 groups of 4 columns
         const int c = grp >> 4, j0 = (grp & 15) * 4;
-        float x[4];
+        f32x4 x;
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int j = j0 + i;
           x[i] = j < c ? sm.X[c * FSTR + j] : (j == c ? 1.f : 0.f);
         }
+        const uint32_t h0 = pack_bf16x2(x[0], x[1]), h1 = pack_bf16x2(x[2], x[3]);
         const int pj = perm(j0);
-        *reinterpret_cast<uint2*>(sm.Th + c * TSTR + pj) =
-            uint2{pack_bf16x2(x[0], x[1]), pack_bf16x2(x[2], x[3])};
-        *reinterpret_cast<uint2*>(sm.Tl + c * TSTR + pj) =
-            uint2{pack_bf16x2(x[0] - bf16_hi(x[0]), x[1] - bf16_hi(x[1])),
-                  pack_bf16x2(x[2] - bf16_hi(x[2]), x[3] - bf16_hi(x[3]))};
+        *reinterpret_cast<uint2*>(sm.Th + c * TSTR + pj) = uint2{h0, h1};
+        *reinterpret_cast<uint2*>(sm.Tl + c * TSTR + pj) = uint2{lo_word(x[0], x[1], h0), lo_word(x[2], x[3], h1)};
       }
       __syncthreads();
 
@@ -340,10 +358,7 @@ __global__ __launch_bounds__(NTHREADS) void gdn_prefill_kernel(PrefillArgs p) {
 #pragma unroll
       for (int vt = 0; vt < 2; ++vt)
 #pragma unroll
-        for (int ks = 0; ks < 4; ++ks) {
-          Sh[vt][ks] = pack_hi(S[vt][2 * ks], S[vt][2 * ks + 1]);
-          Sl[vt][ks] = pack_lo(S[vt][2 * ks], S[vt][2 * ks + 1]);
-        }
+        for (int ks = 0; ks < 4; ++ks) split_pack(S[vt][2 * ks], S[vt][2 * ks + 1], Sh[vt][ks], Sl[vt][ks]);
 
       // X = K S^T and Q S^T for this wave's 32 columns v (rows c of 4 tiles).
       f32x4 Xk[4][2], Xq[4][2];
@@ -366,19 +381,18 @@ __global__ __launch_bounds__(NTHREADS) void gdn_prefill_kernel(PrefillArgs p) {
       }
 
       // Y = beta (V - e^gamma X); element (c = 16ct + 4g + i, v = 32w + 16vt + n16).
+      // The inter term e^gamma_c (Q S^T)[c] is scaled here too.
 #pragma unroll
       for (int ct = 0; ct < 4; ++ct)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
           const int c = 16 * ct + 4 * g + i;
-          const float bc = sm.bet[c], ec = expf(sm.gam[c]);
+          const float bc = sm.bet[c], ec = sm.eg[c];
 #pragma unroll
           for (int vt = 0; vt < 2; ++vt) {
-            float vval = 0.f;
-            if (c < clen)
-              vval = bf16_to_f32(p.v[(cs + c) * vv_stride + int64_t(h) * D + 32 * wave + 16 * vt + n16]);
+            const float vval = bf16_to_f32(sm.V[c * KSTR + 32 * wave + 16 * vt + n16]);
             Xk[ct][vt][i] = bc * (vval - ec * Xk[ct][vt][i]);
-            Xq[ct][vt][i] *= ec;   // inter term e^gamma_c (Q S^T)[c]
+            Xq[ct][vt][i] *= ec;
           }
         }
 
@@ -387,17 +401,14 @@ __global__ __launch_bounds__(NTHREADS) void gdn_prefill_kernel(PrefillArgs p) {
 #pragma unroll
       for (int vt = 0; vt < 2; ++vt)
 #pragma unroll
-        for (int js = 0; js < 2; ++js) {
-          Yh[vt][js] = pack_hi(Xk[2 * js][vt], Xk[2 * js + 1][vt]);
-          Yl[vt][js] = pack_lo(Xk[2 * js][vt], Xk[2 * js + 1][vt]);
-        }
+        for (int js = 0; js < 2; ++js) split_pack(Xk[2 * js][vt], Xk[2 * js + 1][vt], Yh[vt][js], Yl[vt][js]);
       f32x4 Vn[4][2];
 #pragma unroll
       for (int ct = 0; ct < 4; ++ct) {
 #pragma unroll
         for (int vt = 0; vt < 2; ++vt) Vn[ct][vt] = zero4();
 #pragma unroll
-        for (int js = 0; js < 2; ++js) {
+        for (int js = 0; js <= (ct >> 1); ++js) {     // T~ is lower triangular
           const uint4 th = frag(sm.Th, TSTR, 16 * ct, js, lane);
           const uint4 tl = frag(sm.Tl, TSTR, 16 * ct, js, lane);
 #pragma unroll
@@ -409,7 +420,7 @@ __global__ __launch_bounds__(NTHREADS) void gdn_prefill_kernel(PrefillArgs p) {
         }
       }
 
-      // o = scale (e^gamma Q S^T + P v_new)
+      // o = scale (e^gamma Q S^T + P v_new), staged in LDS for coalesced stores.
       uint4 Vb[2][2];
 #pragma unroll
       for (int vt = 0; vt < 2; ++vt)
@@ -418,43 +429,28 @@ __global__ __launch_bounds__(NTHREADS) void gdn_prefill_kernel(PrefillArgs p) {
 #pragma unroll
       for (int ct = 0; ct < 4; ++ct) {
 #pragma unroll
-        for (int js = 0; js < 2; ++js) {
+        for (int js = 0; js <= (ct >> 1); ++js) {     // P is lower triangular
           const uint4 pa = frag(sm.P, TSTR, 16 * ct, js, lane);
 #pragma unroll
           for (int vt = 0; vt < 2; ++vt) Xq[ct][vt] = mfma(pa, Vb[vt][js], Xq[ct][vt]);
         }
+#pragma unroll
+        for (int i = 0; i < 4; ++i)
+#pragma unroll
+          for (int vt = 0; vt < 2; ++vt)
+            sm.O[(16 * ct + 4 * g + i) * KSTR + 32 * wave + 16 * vt + n16] = f32_to_bf16(p.scale * Xq[ct][vt][i]);
       }
-#pragma unroll
-      for (int ct = 0; ct < 4; ++ct)
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const int c = 16 * ct + 4 * g + i;
-          if (c < clen) {
-#pragma unroll
-            for (int vt = 0; vt < 2; ++vt)
-              p.out[(cs + c) * vv_stride + int64_t(h) * D + 32 * wave + 16 * vt + n16] =
-                  f32_to_bf16(p.scale * Xq[ct][vt][i]);
-          }
-        }
 
       // S = e^{gamma_last} S + sum_c K[c]^T (d_c v_new[c]),  d_c = e^{gamma_last - gamma_c}
-      const float glast = sm.gam[clen - 1];
-      const float dlast = expf(glast);
+      const float dlast = sm.eg[clen - 1];
       uint4 Uh[2][2], Ul[2][2];
 #pragma unroll
       for (int js = 0; js < 2; ++js) {
-        f32x4 d0, d1;
+        const float4 d0 = *reinterpret_cast<const float4*>(sm.dd + 32 * js + 4 * g);
+        const float4 d1 = *reinterpret_cast<const float4*>(sm.dd + 32 * js + 16 + 4 * g);
+        const f32x4 e0 = {d0.x, d0.y, d0.z, d0.w}, e1 = {d1.x, d1.y, d1.z, d1.w};
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          d0[i] = expf(glast - sm.gam[32 * js + 4 * g + i]);
-          d1[i] = expf(glast - sm.gam[32 * js + 16 + 4 * g + i]);
-        }
-#pragma unroll
-        for (int vt = 0; vt < 2; ++vt) {
-          const f32x4 u0 = Vn[2 * js][vt] * d0, u1 = Vn[2 * js + 1][vt] * d1;
-          Uh[vt][js] = pack_hi(u0, u1);
-          Ul[vt][js] = pack_lo(u0, u1);
-        }
+        for (int vt = 0; vt < 2; ++vt) split_pack(Vn[2 * js][vt] * e0, Vn[2 * js + 1][vt] * e1, Uh[vt][js], Ul[vt][js]);
       }
 #pragma unroll
       for (int kt = 0; kt < 8; ++kt) {
@@ -469,6 +465,16 @@ __global__ __launch_bounds__(NTHREADS) void gdn_prefill_kernel(PrefillArgs p) {
             S[vt][kt] = mfma(ak, Ul[vt][js], S[vt][kt]);
           }
         }
+      }
+
+      __syncthreads();  // output tile complete
+#pragma unroll
+      for (int it = 0; it < 4; ++it) {
+        const int seg = tid + it * NTHREADS;
+        const int c = seg >> 4, sg = seg & 15;
+        if (c < clen)
+          *reinterpret_cast<uint4*>(p.out + (cs + c) * v_stride + int64_t(h) * D + 8 * sg) =
+              *reinterpret_cast<const uint4*>(sm.O + c * KSTR + 8 * sg);
       }
     }
   }
