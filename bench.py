@@ -51,29 +51,89 @@ def parse():
     ap.add_argument("--only", choices=["decode", "prefill", "all"], default="all")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
+    ap.add_argument("--pmc-run", action="store_true",
+                    help="short fixed launch sequence for rocprofv3 --pmc runs: a torch copy of "
+                         "COPY_BYTES (counter calibration), then 5 decode B=64 launches and 2 "
+                         "prefill launches of the 32k varlen batch; prints nothing")
     return ap.parse_args()
 
 
-def timed_launches(fn, steps, warmup, torch):
-    """Warm up, then time exactly ``steps`` launches.  Returns (wall seconds for
-    the steps between two synchronisations, mean per-launch GPU ms from HIP events
-    recorded on the launch stream)."""
+COPY_BYTES = 1 << 28   # 256 MiB read + 256 MiB written by the calibration copy
+
+
+def pmc_run(torch, binding, workloads):
+    dev = torch.device("cuda:0")
+    src = torch.ones(COPY_BYTES // 4, dtype=torch.float32, device=dev)
+    dst = torch.empty_like(src)
+    flush = torch.empty(COPY_BYTES // 4, dtype=torch.float32, device=dev)
+    for _ in range(3):
+        flush.fill_(1.0)
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    w = workloads.decode_inputs(64, seed=1, device=dev)
+    states = [w["state"]] + [w["state"].clone() for _ in range(3)]
+    out = torch.empty_like(w["v"])
+    for i in range(5):
+        flush.fill_(1.0)
+        st = states[i % 4]
+        binding.decode_kernel(w["q"], w["k"], w["v"], st, w["A_log"], w["a"], w["dt_bias"],
+                              w["b"], w["scale"], out, st)
+    torch.cuda.synchronize()
+    p = workloads.config(4, device=dev)
+    po = torch.empty((p["q"].shape[0], HV, D), dtype=torch.bfloat16, device=dev)
+    ns = torch.empty_like(p["state"])
+    for _ in range(2):
+        flush.fill_(1.0)
+        binding.prefill_kernel(p["q"], p["k"], p["v"], p["state"], p["A_log"], p["a"],
+                               p["dt_bias"], p["b"], p["cu_seqlens"], p["scale"], po, ns)
+    torch.cuda.synchronize()
+
+
+def timed_launches(fn, steps, warmup, torch, use_graph=False):
+    """Warm up, then time exactly ``steps`` launches of ``fn(i)``.
+
+    With ``use_graph`` the ``steps`` launches are captured once into a HIP graph
+    (torch.cuda.CUDAGraph on the current device), replayed once untimed, and the
+    timed region is one replay; otherwise they are launched eagerly.  Returns
+    (wall seconds between two synchronisations, mean ms per launch from a HIP
+    event pair recorded on the launch stream around the timed region, mode)."""
     for i in range(warmup):
         fn(i)
     torch.cuda.synchronize()
+    graph, mode = None, "eager"
+    if use_graph:
+        try:
+            side = torch.cuda.Stream()
+            side.wait_stream(torch.cuda.current_stream())
+            with torch.cuda.stream(side):
+                fn(0)
+            torch.cuda.current_stream().wait_stream(side)
+            torch.cuda.synchronize()
+            graph = torch.cuda.CUDAGraph()
+            with torch.cuda.graph(graph):
+                for i in range(steps):
+                    fn(warmup + i)
+            graph.replay()
+            torch.cuda.synchronize()
+            mode = "hipGraph"
+        except Exception as exc:          # capture unsupported: fall back to eager launches
+            print(f"bench.py: graph capture failed ({exc}); timing eager launches",
+                  file=sys.stderr)
+            graph = None
     stream = torch.cuda.current_stream()
-    ev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
-          for _ in range(steps)]
+    start, end = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     torch.cuda.synchronize()
     t0 = time.perf_counter()
-    for i in range(steps):
-        ev[i][0].record(stream)
-        fn(warmup + i)
-        ev[i][1].record(stream)
+    start.record(stream)
+    if graph is not None:
+        graph.replay()
+    else:
+        for i in range(steps):
+            fn(warmup + i)
+    end.record(stream)
     torch.cuda.synchronize()
     wall = time.perf_counter() - t0
-    per = [a.elapsed_time(b) for a, b in ev]
-    return wall, float(np.mean(per)), float(np.median(per))
+    return wall, start.elapsed_time(end) / steps, mode
 
 
 def bench_decode(args, torch, binding, workloads):
@@ -89,9 +149,10 @@ def bench_decode(args, torch, binding, workloads):
         binding.decode_kernel(w["q"], w["k"], w["v"], st, w["A_log"], w["a"], w["dt_bias"],
                               w["b"], w["scale"], out, st)
 
-    wall, ev_mean, ev_med = timed_launches(step, args.steps, args.warmup, torch)
-    nbytes = decode_bytes(B)
-    return dict(bytes=nbytes, wall=wall, ev_mean_ms=ev_mean, ev_med_ms=ev_med)
+    wall, ev_ms, mode = timed_launches(step, args.steps, args.warmup, torch, use_graph=True)
+    wall_e, ev_ms_e, _ = timed_launches(step, args.steps, 0, torch, use_graph=False)
+    return dict(bytes=decode_bytes(B), wall=wall, ev_ms=ev_ms, mode=mode, eager_wall=wall_e,
+                eager_ev_ms=ev_ms_e)
 
 
 def bench_pooled(args, torch, binding, workloads):
@@ -104,7 +165,7 @@ def bench_pooled(args, torch, binding, workloads):
                                      w["dt_bias"], w["b"], w["scale"], out, w["state_indices"])
 
     steps = max(5, args.steps // 2)
-    wall, ev_mean, ev_med = timed_launches(step, steps, min(args.warmup, 3), torch)
+    wall, ev_mean, _ = timed_launches(step, steps, min(args.warmup, 3), torch)
     nbytes = decode_bytes(512, slots_idx=True)
     return dict(us=ev_mean * 1e3, gbs=nbytes / (ev_mean * 1e-3) / 1e9,
                 frac=nbytes / (ev_mean * 1e-3) / 1e9 / HBM_PEAK_GBS, bytes=nbytes)
@@ -123,7 +184,7 @@ def bench_prefill(args, torch, binding, workloads, cfg):
                                p["dt_bias"], p["b"], p["cu_seqlens"], p["scale"], out, ns)
 
     steps = max(3, args.steps // 5)
-    wall, ev_mean, ev_med = timed_launches(step, steps, min(args.warmup, 2), torch)
+    wall, ev_mean, _ = timed_launches(step, steps, min(args.warmup, 2), torch)
     flop = HV * T * PREFILL_FLOP_PER_TOKEN_HEAD
     tfs = flop / (ev_mean * 1e-3) / 1e12
     return dict(tokens=T, seqs=N, us=ev_mean * 1e3, tokens_per_s=T / (ev_mean * 1e-3),
@@ -189,6 +250,9 @@ def main():
     from gdn_kernel_amd import binding, workloads, _lib
     _lib.load()
     assert torch.cuda.is_available(), "no ROCm GPU visible"
+    if args.pmc_run:
+        pmc_run(torch, binding, workloads)
+        return
 
     res = {"metric": "GDN decode µs + HBM GB/s at B=64; prefill tokens/s (32k varlen), 1 GPU",
            "value": None, "unit": "GB/s", "n_gpus": 1, "steps": args.steps,
@@ -201,11 +265,13 @@ def main():
     if args.only in ("decode", "all"):
         d = bench_decode(args, torch, binding, workloads)
         gbs_wall = d["bytes"] * args.steps / d["wall"] / 1e9
-        gbs_kernel = d["bytes"] / (d["ev_mean_ms"] * 1e-3) / 1e9
+        gbs_kernel = d["bytes"] / (d["ev_ms"] * 1e-3) / 1e9
         res["value"] = round(gbs_wall, 1)
         res["ms_per_step"] = round(d["wall"] / args.steps * 1e3, 5)
-        res["decode_us"] = round(d["ev_mean_ms"] * 1e3, 2)
-        res["decode_us_median"] = round(d["ev_med_ms"] * 1e3, 2)
+        res["decode_us"] = round(d["ev_ms"] * 1e3, 2)
+        res["launch"] = d["mode"]
+        res["decode_eager"] = {"us_per_launch": round(d["eager_ev_ms"] * 1e3, 2),
+                               "wall_gbs": round(d["bytes"] * args.steps / d["eager_wall"] / 1e9, 1)}
         res["roofline"] = {"bound": "hbm", "achieved": round(gbs_kernel, 1),
                            "peak": HBM_PEAK_GBS, "unit": "GB/s",
                            "frac": round(gbs_kernel / HBM_PEAK_GBS, 4),

@@ -37,7 +37,14 @@ _BF16 = torch.bfloat16
 _F32 = torch.float32
 
 
-def _need(t: torch.Tensor, name: str, dtype: torch.dtype, shape: tuple, device) -> None:
+def _need(t, name: str, dtype: torch.dtype, shape: tuple, device) -> None:
+    # Fast path first: one attribute read per property, no allocation.
+    try:
+        if (t.dtype is dtype and t.shape == shape and t.device == device
+                and t.is_contiguous()):
+            return
+    except AttributeError:
+        raise ValueError(f"{name} must be a torch.Tensor") from None
     if not isinstance(t, torch.Tensor):
         raise ValueError(f"{name} must be a torch.Tensor")
     if t.dtype != dtype:
@@ -46,8 +53,27 @@ def _need(t: torch.Tensor, name: str, dtype: torch.dtype, shape: tuple, device) 
         raise ValueError(f"{name} must have shape {tuple(shape)} (got {tuple(t.shape)})")
     if t.device != device:
         raise ValueError(f"{name} is on {t.device}, expected {device}")
-    if not t.is_contiguous():
-        raise ValueError(f"{name} must be contiguous")
+    raise ValueError(f"{name} must be contiguous")
+
+
+class _on_device:
+    """Make ``device`` current for the call; a no-op when it already is."""
+
+    __slots__ = ("idx", "prev")
+
+    def __init__(self, device: torch.device):
+        self.idx = device.index if device.index is not None else torch.cuda.current_device()
+
+    def __enter__(self):
+        self.prev = torch.cuda.current_device()
+        if self.prev != self.idx:
+            torch.cuda.set_device(self.idx)
+        return self
+
+    def __exit__(self, *exc):
+        if self.prev != self.idx:
+            torch.cuda.set_device(self.prev)
+        return False
 
 
 def _device_of(q: torch.Tensor) -> torch.device:
@@ -95,7 +121,7 @@ def decode_kernel(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state
     _need(output, "output", _BF16, (B, 1, Hv, dv), dev)
     _need(new_state, "new_state", _F32, (B, Hv, dv, dk), dev)
     lib = _lib.load()
-    with torch.cuda.device(dev):
+    with _on_device(dev):
         rc = lib.gdn_decode(_ptr(q), _ptr(k), _ptr(v), _ptr(state), _ptr(A_log), _ptr(a),
                             _ptr(dt_bias), _ptr(b), _scale(scale), _ptr(output), _ptr(new_state),
                             B, Hq, Hk, Hv, dk, dv, _stream(dev))
@@ -130,7 +156,7 @@ def decode_pooled_kernel(q, k, v, state_pool, A_log, a, dt_bias, b, scale, outpu
     _need(b, "b", _BF16, (B, 1, Hv), dev)
     _need(output, "output", _BF16, (B, 1, Hv, dv), dev)
     lib = _lib.load()
-    with torch.cuda.device(dev):
+    with _on_device(dev):
         rc = lib.gdn_decode_pooled(_ptr(q), _ptr(k), _ptr(v), _ptr(state_pool), slots,
                                    _ptr(state_indices), _ptr(A_log), _ptr(a), _ptr(dt_bias),
                                    _ptr(b), _scale(scale), _ptr(output), B, Hq, Hk, Hv, dk, dv,
@@ -182,7 +208,7 @@ def prefill_kernel(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, outp
     _need(output, "output", _BF16, (T, Hv, dv), dev)
     _need(new_state, "new_state", _F32, (N, Hv, dv, dk), dev)
     lib = _lib.load()
-    with torch.cuda.device(dev):
+    with _on_device(dev):
         rc = lib.gdn_prefill(_ptr(q), _ptr(k), _ptr(v), _ptr(state), _ptr(A_log), _ptr(a),
                              _ptr(dt_bias), _ptr(b), cu_seqlens.data_ptr(), cu_code, N, T,
                              _scale(scale), _ptr(output), _ptr(new_state), Hq, Hk, Hv, dk, dv,

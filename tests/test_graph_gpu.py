@@ -1,0 +1,76 @@
+"""HIP-graph capture of the decode and prefill launches: every replay (with eager
+work and synchronisations in between) must reproduce the eager result bit for bit."""
+import pytest
+import torch
+
+from gdn_kernel_amd import binding, workloads
+from tests.gpu_util import say
+
+pytestmark = pytest.mark.gpu
+
+
+def _capture(fn):
+    side = torch.cuda.Stream()
+    side.wait_stream(torch.cuda.current_stream())
+    with torch.cuda.stream(side):
+        fn()
+    torch.cuda.current_stream().wait_stream(side)
+    torch.cuda.synchronize()
+    g = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(g):
+        fn()
+    return g
+
+
+def test_decode_graph_replays_match_eager(gpu):
+    say("decode graph replay")
+    w = workloads.decode_inputs(16, seed=31, device=gpu, gate="slow", state_scale=0.5)
+    out = torch.empty_like(w["v"])
+    ns = torch.empty_like(w["state"])
+
+    def step():
+        binding.decode_kernel(w["q"], w["k"], w["v"], w["state"], w["A_log"], w["a"],
+                              w["dt_bias"], w["b"], w["scale"], out, ns)
+
+    step()
+    torch.cuda.synchronize()
+    ref_o, ref_s = out.clone(), ns.clone()
+    g = _capture(step)
+    for rep in range(4):
+        out.fill_(float("nan"))
+        ns.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref_o), f"replay {rep}: output differs"
+        assert torch.equal(ns, ref_s), f"replay {rep}: state differs"
+        x = torch.randn(1 << 20, device=gpu).sum()        # unrelated eager work in between
+        assert torch.isfinite(x)
+
+
+def test_prefill_graph_replays_match_eager(gpu):
+    say("prefill graph replay")
+    p = workloads.prefill_inputs([130, 3, 0, 64], seed=32, device=gpu, gate="slow",
+                                 state_scale=0.5)
+    T, N = p["q"].shape[0], len(p["lengths"])
+    out = torch.empty((T, 32, 128), dtype=torch.bfloat16, device=gpu)
+    ns = torch.empty((N, 32, 128, 128), dtype=torch.float32, device=gpu)
+
+    def step():
+        binding.prefill_kernel(p["q"], p["k"], p["v"], p["state"], p["A_log"], p["a"],
+                               p["dt_bias"], p["b"], p["cu_seqlens"], p["scale"], out, ns)
+
+    step()
+    torch.cuda.synchronize()
+    ref_o, ref_s = out.clone(), ns.clone()
+    g = _capture(step)
+    for rep in range(3):
+        out.zero_()
+        ns.fill_(float("nan"))
+        torch.cuda.synchronize()
+        g.replay()
+        torch.cuda.synchronize()
+        assert torch.equal(out, ref_o), f"replay {rep}: output differs"
+        assert torch.equal(ns, ref_s), f"replay {rep}: state differs"
+        step()                                               # eager call between replays
+        torch.cuda.synchronize()
