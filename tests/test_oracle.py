@@ -4,8 +4,9 @@ The reference ships no golden vectors or tests for this path, so each oracle
 function is checked against closed forms, invariants and independent
 restatements (the paper's matrix recurrence, the FLA recurrent and chunk forms,
 the reference kernel's per-chunk algorithm) -- chosen so that a plausible
-mistake fails at least one check.  ``TestMutants`` plants such mistakes in
-wrappers around the oracle and confirms the checks catch them.
+mistake fails at least one check.  The mutant tests plant such mistakes in
+wrappers around the oracle and confirms the checks catch them (the
+``test_*_catch_*`` tests).
 """
 import math
 
