@@ -20,9 +20,9 @@
 // Work split inside a chunk (all waves in parallel between barriers):
 //   A: wave 0 -- the four diagonal 16x16 blocks of N and their inverses (VALU
 //      forward substitution); waves 1, 2 -- the off-diagonal blocks of N (bf16
-//      hi/lo) and P; wave 3 -- its X = K S^T and Q S^T.
+//      hi/lo) and P; wave 3 -- two blocks of P and its X = K S^T.
 //   B: wave 3 -- the off-diagonal blocks of T~ by block recursion on MFMA;
-//      waves 0-2 -- their X = K S^T and Q S^T.
+//      waves 0-2 -- their X = K S^T; wave 1 also the next chunk's gates.
 //   C: every wave -- Y, v_new, the output, the state update; the next chunk's
 //      inputs are loaded into registers meanwhile.
 //
@@ -69,10 +69,12 @@ struct __align__(16) PrefillSmem {
   uint16_t Nh[C * TSTR];      // off-diagonal blocks of N, hi [i][perm(j)]
   uint16_t Nl[C * TSTR];      // off-diagonal blocks of N, lo
   float Nd[4 * 16 * DSTR];    // diagonal 16x16 blocks of N (fp32)
-  float gam[C];               // gamma_c (inclusive cumsum of the log gates)
-  float bet[C];               // beta_c
-  float eg[C];                // e^{gamma_c}
-  float dd[C];                // e^{gamma_last - gamma_c}
+  // Per-chunk gate values, double-buffered (chunk parity): the next chunk's are
+  // written while the current chunk's are read.
+  float gam[2][C];            // gamma_c (inclusive cumsum of the log gates)
+  float bet[2][C];            // beta_c
+  float eg[2][C];             // e^{gamma_c}
+  float dd[2][C];             // e^{gamma_last - gamma_c}
   int seq;                    // sequence handled by this workgroup
 };
 
@@ -175,24 +177,26 @@ struct TileJob {
   int kind, I, J;
 };
 
-__device__ __forceinline__ void tile_epilogue(PrefillSmem& sm, const TileJob t, const f32x4& acc, int lane) {
+__device__ __forceinline__ void tile_epilogue(PrefillSmem& sm, int buf, const TileJob t, const f32x4& acc, int lane) {
   const int g = lane >> 4, n16 = lane & 15;
+  const float* gam = sm.gam[buf];
+  const float* bet = sm.bet[buf];
   if (t.kind == 0) {
     // acc[i] = k_r . k_c, r = 16I + 4g + i, c = 16I + n16
     const int c = 16 * t.I + n16;
-    const float gc = sm.gam[c];
+    const float gc = gam[c];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int ri = 4 * g + i, r = 16 * t.I + ri;
-      sm.Nd[(t.I * 16 + ri) * DSTR + n16] = ri > n16 ? sm.bet[r] * exp_le0(sm.gam[r] - gc) * acc[i] : 0.f;
+      sm.Nd[(t.I * 16 + ri) * DSTR + n16] = ri > n16 ? bet[r] * exp_le0(gam[r] - gc) * acc[i] : 0.f;
     }
   } else if (t.kind == 1) {
     // acc[i] = k_c . k_r, c = 16J + 4g + i, r = 16I + n16  ->  N[r][c]
     const int r = 16 * t.I + n16;
-    const float gr = sm.gam[r], br = sm.bet[r];
+    const float gr = gam[r], br = bet[r];
     f32x4 x;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) x[i] = br * exp_le0(gr - sm.gam[16 * t.J + 4 * g + i]) * acc[i];
+    for (int i = 0; i < 4; ++i) x[i] = br * exp_le0(gr - gam[16 * t.J + 4 * g + i]) * acc[i];
     uint2 hi, lo;
     split4(x, hi, lo);
     const int pos = r * TSTR + perm(16 * t.J + 4 * g);
@@ -201,12 +205,12 @@ __device__ __forceinline__ void tile_epilogue(PrefillSmem& sm, const TileJob t, 
   } else {
     // acc[i] = k_j . q_c, j = 16J + 4g + i, c = 16I + n16  ->  P[c][j]
     const int c = 16 * t.I + n16;
-    const float gc = sm.gam[c];
+    const float gc = gam[c];
     float pv[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
       const int j = 16 * t.J + 4 * g + i;
-      pv[i] = j <= c ? exp_le0(gc - sm.gam[j]) * acc[i] : 0.f;
+      pv[i] = j <= c ? exp_le0(gc - gam[j]) * acc[i] : 0.f;
     }
     *reinterpret_cast<uint2*>(sm.P + c * TSTR + perm(16 * t.J + 4 * g)) =
         uint2{pack_bf16x2(pv[0], pv[1]), pack_bf16x2(pv[2], pv[3])};
@@ -214,7 +218,7 @@ __device__ __forceinline__ void tile_epilogue(PrefillSmem& sm, const TileJob t, 
 }
 
 template <int NJ>
-__device__ __forceinline__ void run_tiles(PrefillSmem& sm, const TileJob (&jobs)[NJ], int lane) {
+__device__ __forceinline__ void run_tiles(PrefillSmem& sm, int buf, const TileJob (&jobs)[NJ], int lane) {
   f32x4 acc[NJ];
 #pragma unroll
   for (int t = 0; t < NJ; ++t) acc[t] = zero4();
@@ -230,7 +234,7 @@ __device__ __forceinline__ void run_tiles(PrefillSmem& sm, const TileJob (&jobs)
     }
   }
 #pragma unroll
-  for (int t = 0; t < NJ; ++t) tile_epilogue(sm, jobs[t], acc[t], lane);
+  for (int t = 0; t < NJ; ++t) tile_epilogue(sm, buf, jobs[t], acc[t], lane);
 }
 
 // ---------------------------------------------------------------------------
@@ -246,11 +250,14 @@ __device__ __forceinline__ void solve_diagonal(PrefillSmem& sm, int lane) {
   for (int i = 0; i < 16; ++i) x[i] = (i == j) ? 1.f : 0.f;
 #pragma unroll
   for (int i = 1; i < 16; ++i) {
-    float acc = 0.f;
+    float acc0 = 0.f, acc1 = 0.f;   // two partial sums halve the dependent FMA chain
 #pragma unroll
-    for (int m = 0; m < i; ++m) acc += nb[i * DSTR + m] * x[m];
-    if (i > j) x[i] = -acc;
-    __builtin_amdgcn_sched_barrier(0);  // keep each row's LDS reads next to its FMAs
+    for (int m = 0; m < i; m += 2) {
+      acc0 += nb[i * DSTR + m] * x[m];
+      if (m + 1 < i) acc1 += nb[i * DSTR + m + 1] * x[m + 1];
+    }
+    if (i > j) x[i] = -(acc0 + acc1);
+    if (i & 1) __builtin_amdgcn_sched_barrier(0);  // bound hoisted LDS reads to ~two rows
   }
   const int col = perm(16 * I + j);
 #pragma unroll
@@ -330,46 +337,65 @@ __device__ __forceinline__ void solve_offdiagonal(PrefillSmem& sm, int lane) {
   finish_block(sm, g30, 3, 0, lane);
 }
 
-// X = K S^T (rows c, cols v: Xk[ct][vt]) and Q S^T transposed (rows v, cols c:
-// Xq[vt][ct]) for this wave's 32 state rows.  S enters as hi/lo B operands for
-// K S^T and as the hi A operand for S Q^T.
-__device__ __forceinline__ void state_products(const PrefillSmem& sm, const f32x4 (&S)[2][8], f32x4 (&Xk)[4][2],
-                                               f32x4 (&Xq)[2][4], int lane) {
-  uint4 Sh[2][4], Sl[2][4];
+// X = K S^T (rows c, cols v: Xk[ct][vt]) for this wave's 32 state rows; S
+// enters as hi/lo B operands.
+__device__ __forceinline__ void retrieve(const PrefillSmem& sm, const f32x4 (&S)[2][8], f32x4 (&Xk)[4][2], int lane) {
 #pragma unroll
-  for (int vt = 0; vt < 2; ++vt)
+  for (int ct = 0; ct < 4; ++ct)
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) split_pack(S[vt][2 * ks], S[vt][2 * ks + 1], Sh[vt][ks], Sl[vt][ks]);
+    for (int vt = 0; vt < 2; ++vt) Xk[ct][vt] = zero4();
 #pragma unroll
-  for (int ct = 0; ct < 4; ++ct) {
+  for (int ks = 0; ks < 4; ++ks) {
+    uint4 Sh[2], Sl[2];
 #pragma unroll
-    for (int vt = 0; vt < 2; ++vt) { Xk[ct][vt] = zero4(); Xq[vt][ct] = zero4(); }
+    for (int vt = 0; vt < 2; ++vt) split_pack(S[vt][2 * ks], S[vt][2 * ks + 1], Sh[vt], Sl[vt]);
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks) {
+    for (int ct = 0; ct < 4; ++ct) {
       const uint4 ak = frag(sm.K, KSTR, 16 * ct, ks, lane);
-      const uint4 bq = frag(sm.Q, KSTR, 16 * ct, ks, lane);
 #pragma unroll
       for (int vt = 0; vt < 2; ++vt) {
-        Xk[ct][vt] = mfma(ak, Sh[vt][ks], Xk[ct][vt]);
-        Xk[ct][vt] = mfma(ak, Sl[vt][ks], Xk[ct][vt]);
-        Xq[vt][ct] = mfma(Sh[vt][ks], bq, Xq[vt][ct]);
+        Xk[ct][vt] = mfma(ak, Sh[vt], Xk[ct][vt]);
+        Xk[ct][vt] = mfma(ak, Sl[vt], Xk[ct][vt]);
       }
     }
     __builtin_amdgcn_sched_barrier(0);  // bound the number of operand loads in flight
   }
 }
 
+// (Q S^T)^T (rows v, cols c: Xq[vt][ct]) for this wave's 32 state rows; S enters
+// as the bf16 hi A operand (output-only product).
+__device__ __forceinline__ void inter_term(const PrefillSmem& sm, const f32x4 (&S)[2][8], f32x4 (&Xq)[2][4],
+                                           int lane) {
+#pragma unroll
+  for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+    for (int vt = 0; vt < 2; ++vt) Xq[vt][ct] = zero4();
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    uint4 Sh[2];
+#pragma unroll
+    for (int vt = 0; vt < 2; ++vt) Sh[vt] = pack_hi(S[vt][2 * ks], S[vt][2 * ks + 1]);
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) {
+      const uint4 bq = frag(sm.Q, KSTR, 16 * ct, ks, lane);
+#pragma unroll
+      for (int vt = 0; vt < 2; ++vt) Xq[vt][ct] = mfma(Sh[vt], bq, Xq[vt][ct]);
+    }
+  }
+}
+
 struct Prefetch {
   uint4 k[4], q[4], v[4];
-  float a, b;
 };
 
+// This thread's K/Q/V segments of a chunk: segment tid + 256*it is token
+// seg/16, columns 8*(seg%16) .. +7, so 16 consecutive threads read one
+// contiguous 256-byte row.
 __device__ __forceinline__ void prefetch_chunk(const PrefillArgs& p, int64_t cs, int clen, int h, int hq, int hk,
-                                               int lane, int wave, Prefetch& f) {
-  const int c = lane;
+                                               int tid, Prefetch& f) {
 #pragma unroll
   for (int it = 0; it < 4; ++it) {
-    const int sg = 4 * it + wave;
+    const int seg = tid + it * NTHREADS, c = seg >> 4, sg = seg & 15;
     f.k[it] = f.q[it] = f.v[it] = uint4{0u, 0u, 0u, 0u};
     if (c < clen) {
       f.k[it] = *reinterpret_cast<const uint4*>(p.k + ((cs + c) * p.Hk + hk) * D + 8 * sg);
@@ -377,12 +403,37 @@ __device__ __forceinline__ void prefetch_chunk(const PrefillArgs& p, int64_t cs,
       f.v[it] = *reinterpret_cast<const uint4*>(p.v + ((cs + c) * p.Hv + h) * D + 8 * sg);
     }
   }
-  f.a = f.b = 0.f;
-  if (wave == 0 && lane < clen) {
+}
+
+// Per-token gate values of a chunk, one token per lane of a wavefront, into
+// gate buffer `buf`.
+__device__ __forceinline__ void chunk_gates(PrefillSmem& sm, int buf, float a, float b, float A_log, float dt_bias,
+                                            int clen, int lane) {
+  const float lg = lane < clen ? log_gate(A_log, a, dt_bias) : 0.f;
+  const float bt = lane < clen ? sigmoidf_(b) : 0.f;
+  const float gm = wave_inclusive_scan(lg, lane);
+  const float glast = readlane_f(gm, clen - 1);
+  sm.gam[buf][lane] = gm;
+  sm.bet[buf][lane] = bt;
+  sm.eg[buf][lane] = expf(gm);
+  sm.dd[buf][lane] = expf(glast - gm);
+}
+
+__device__ __forceinline__ void load_ab(const PrefillArgs& p, int64_t cs, int clen, int h, int lane, float& a,
+                                        float& b) {
+  a = b = 0.f;
+  if (lane < clen) {
     const int64_t idx = (cs + lane) * p.Hv + h;
-    f.a = bf16_to_f32(p.a[idx]);
-    f.b = bf16_to_f32(p.b[idx]);
+    a = bf16_to_f32(p.a[idx]);
+    b = bf16_to_f32(p.b[idx]);
   }
+}
+
+// Workgroup barrier ordering LDS only: waits for this wave's LDS operations,
+// not for its outstanding global loads/stores (no global memory is shared
+// between the waves of a workgroup here).
+__device__ __forceinline__ void lds_barrier() {
+  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
 // The sequence of rank `rank` in descending length order (ties: lower index
@@ -462,7 +513,16 @@ __global__ __launch_bounds__(NTHREADS) void gdn_prefill_kernel(PrefillArgs p) {
     const int64_t out_stride = int64_t(p.Hv) * D;
 
     Prefetch f;
-    prefetch_chunk(p, s0, int(s1 - s0 < C ? s1 - s0 : C), h, hq, hk, lane0, wave, f);
+    {
+      const int clen0 = int(s1 - s0 < C ? s1 - s0 : C);
+      prefetch_chunk(p, s0, clen0, h, hq, hk, tid, f);
+      if (wave == 1) {
+        float a, b;
+        load_ab(p, s0, clen0, h, lane0, a, b);
+        chunk_gates(sm, 0, a, b, A_log, dt_bias, clen0, lane0);
+      }
+    }
+    int buf = 0;   // gate buffer of the current chunk
 
     for (int64_t cs = s0; cs < s1; cs += C) {
       const int clen = int(s1 - cs < C ? s1 - cs : C);
@@ -472,12 +532,12 @@ __global__ __launch_bounds__(NTHREADS) void gdn_prefill_kernel(PrefillArgs p) {
       int lane = lane0;
       asm volatile("" : "+v"(lane));
       const int g = lane >> 4, n16 = lane & 15;
-      __syncthreads();  // the previous chunk's LDS reads are done
+      lds_barrier();  // the previous chunk's LDS reads are done
 
       // ---- stage K, Q, V from the prefetched registers; gates ---------------
 #pragma unroll
       for (int it = 0; it < 4; ++it) {
-        const int c = lane, sg = 4 * it + wave;
+        const int seg = tid + it * NTHREADS, c = seg >> 4, sg = seg & 15;
         const int col0 = (8 * sg) & ~31, r0 = (8 * sg) & 31;
         const int pa = col0 + perm32(r0), pb = col0 + perm32(r0 + 4);
         *reinterpret_cast<uint2*>(sm.K + c * KSTR + pa) = uint2{f.k[it].x, f.k[it].y};
@@ -486,52 +546,55 @@ __global__ __launch_bounds__(NTHREADS) void gdn_prefill_kernel(PrefillArgs p) {
         *reinterpret_cast<uint2*>(sm.Q + c * KSTR + pb) = uint2{f.q[it].z, f.q[it].w};
         *reinterpret_cast<uint4*>(sm.V + c * KSTR + 8 * sg) = f.v[it];
       }
-      if (wave == 0) {
-        const float lg = lane < clen ? log_gate(A_log, f.a, dt_bias) : 0.f;
-        const float bt = lane < clen ? sigmoidf_(f.b) : 0.f;
-        const float gm = wave_inclusive_scan(lg, lane);
-        const float glast = readlane_f(gm, clen - 1);
-        sm.gam[lane] = gm;
-        sm.bet[lane] = bt;
-        sm.eg[lane] = expf(gm);
-        sm.dd[lane] = expf(glast - gm);
-      }
-      __syncthreads();
+      lds_barrier();
+      const float* gam = sm.gam[buf];
+      const float* bet = sm.bet[buf];
+      const float* egv = sm.eg[buf];
+      const float* ddv = sm.dd[buf];
 
-      f32x4 Xk[4][2], Xq[2][4];
+      // Next chunk's gate inputs (wave 1): loaded now, turned into gates in phase B.
+      const int64_t nc = cs + C;
+      const int nclen = int(s1 - nc < C ? s1 - nc : C);
+      float na = 0.f, nb = 0.f;
+      if (wave == 1 && nc < s1) load_ab(p, nc, nclen, h, lane, na, nb);
+
+      f32x4 Xk[4][2];
       // ---- phase A -------------------------------------------------------------
       if (wave == 0) {
         const TileJob jobs[4] = {{0, 0, 0}, {0, 1, 1}, {0, 2, 2}, {0, 3, 3}};
-        run_tiles(sm, jobs, lane);
+        run_tiles(sm, buf, jobs, lane);
         wave_lds_sync();
         solve_diagonal(sm, lane);
       } else if (wave == 1) {
         const TileJob jobs[8] = {{1, 1, 0}, {1, 2, 0}, {1, 3, 0}, {1, 2, 1},
                                  {1, 3, 1}, {1, 3, 2}, {2, 0, 0}, {2, 1, 1}};
-        run_tiles(sm, jobs, lane);
+        run_tiles(sm, buf, jobs, lane);
       } else if (wave == 2) {
-        const TileJob jobs[8] = {{2, 1, 0}, {2, 2, 0}, {2, 2, 1}, {2, 2, 2},
-                                 {2, 3, 0}, {2, 3, 1}, {2, 3, 2}, {2, 3, 3}};
-        run_tiles(sm, jobs, lane);
+        const TileJob jobs[6] = {{2, 1, 0}, {2, 2, 0}, {2, 2, 1}, {2, 2, 2}, {2, 3, 0}, {2, 3, 1}};
+        run_tiles(sm, buf, jobs, lane);
       } else {
-        state_products(sm, S, Xk, Xq, lane);
+        const TileJob jobs[2] = {{2, 3, 2}, {2, 3, 3}};
+        run_tiles(sm, buf, jobs, lane);
+        retrieve(sm, S, Xk, lane);
       }
-      __syncthreads();
+      lds_barrier();
 
       // ---- phase B -------------------------------------------------------------
       if (wave == 3) {
         solve_offdiagonal(sm, lane);
       } else {
-        state_products(sm, S, Xk, Xq, lane);
+        retrieve(sm, S, Xk, lane);
+        // Next chunk's gates, into the other gate buffer.
+        if (wave == 1 && nc < s1) chunk_gates(sm, buf ^ 1, na, nb, A_log, dt_bias, nclen, lane);
       }
-      __syncthreads();
+      lds_barrier();
 
       // ---- phase C: Y, v_new, output, state update -------------------------------
       // Y = beta (V - e^gamma X); element (c = 16ct + 4g + i, v = 32w + 16vt + n16).
 #pragma unroll
       for (int ct = 0; ct < 4; ++ct) {
-        const float4 bc = *reinterpret_cast<const float4*>(sm.bet + 16 * ct + 4 * g);
-        const float4 ec = *reinterpret_cast<const float4*>(sm.eg + 16 * ct + 4 * g);
+        const float4 bc = *reinterpret_cast<const float4*>(bet + 16 * ct + 4 * g);
+        const float4 ec = *reinterpret_cast<const float4*>(egv + 16 * ct + 4 * g);
         const float b4[4] = {bc.x, bc.y, bc.z, bc.w}, e4[4] = {ec.x, ec.y, ec.z, ec.w};
 #pragma unroll
         for (int vt = 0; vt < 2; ++vt) {
@@ -540,10 +603,6 @@ __global__ __launch_bounds__(NTHREADS) void gdn_prefill_kernel(PrefillArgs p) {
 #pragma unroll
           for (int i = 0; i < 4; ++i) Xk[ct][vt][i] = b4[i] * (vf[i] - e4[i] * Xk[ct][vt][i]);
         }
-        // Inter term of the transposed output (column c = 16ct + n16): e^gamma_c (S Q^T).
-        const float ecn = sm.eg[16 * ct + n16];
-#pragma unroll
-        for (int vt = 0; vt < 2; ++vt) Xq[vt][ct] = Xq[vt][ct] * ecn;
       }
 
       // v_new = T~ Y (contraction over the rows of Y: blocks js; T~ is lower triangular).
@@ -571,6 +630,14 @@ __global__ __launch_bounds__(NTHREADS) void gdn_prefill_kernel(PrefillArgs p) {
       }
 
       // o^T = e^gamma (S Q^T) + v_new^T P^T (rows v, cols c); P is lower triangular.
+      f32x4 Xq[2][4];
+      inter_term(sm, S, Xq, lane);
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct) {
+        const float ecn = egv[16 * ct + n16];   // e^gamma of column c = 16ct + n16
+#pragma unroll
+        for (int vt = 0; vt < 2; ++vt) Xq[vt][ct] = Xq[vt][ct] * ecn;
+      }
 #pragma unroll
       for (int js = 0; js < 2; ++js) {
         uint4 vb[2];
@@ -596,20 +663,15 @@ __global__ __launch_bounds__(NTHREADS) void gdn_prefill_kernel(PrefillArgs p) {
       }
 
       // S = e^{gamma_last} S + sum_c K[c]^T (d_c v_new[c]),  d_c = e^{gamma_last - gamma_c}
-      const float dlast = sm.eg[clen - 1];
+      const float dlast = egv[clen - 1];
       uint4 Uh[2][2], Ul[2][2];
 #pragma unroll
       for (int js = 0; js < 2; ++js) {
-        const float4 d0 = *reinterpret_cast<const float4*>(sm.dd + 32 * js + 4 * g);
-        const float4 d1 = *reinterpret_cast<const float4*>(sm.dd + 32 * js + 16 + 4 * g);
+        const float4 d0 = *reinterpret_cast<const float4*>(ddv + 32 * js + 4 * g);
+        const float4 d1 = *reinterpret_cast<const float4*>(ddv + 32 * js + 16 + 4 * g);
         const f32x4 e0 = {d0.x, d0.y, d0.z, d0.w}, e1 = {d1.x, d1.y, d1.z, d1.w};
 #pragma unroll
         for (int vt = 0; vt < 2; ++vt) split_pack(Vn[2 * js][vt] * e0, Vn[2 * js + 1][vt] * e1, Uh[vt][js], Ul[vt][js]);
-      }
-      // Next chunk's inputs, in flight during the state update.
-      if (cs + C < s1) {
-        const int64_t nc = cs + C;
-        prefetch_chunk(p, nc, int(s1 - nc < C ? s1 - nc : C), h, hq, hk, lane, wave, f);
       }
 #pragma unroll
       for (int kt = 0; kt < 8; ++kt) {
@@ -626,7 +688,9 @@ __global__ __launch_bounds__(NTHREADS) void gdn_prefill_kernel(PrefillArgs p) {
         }
       }
 
-      __syncthreads();  // output tile complete
+      lds_barrier();  // output tile complete
+      // Next chunk's K/Q/V, in flight during the output store and the barrier.
+      if (nc < s1) prefetch_chunk(p, nc, nclen, h, hq, hk, tid, f);
 #pragma unroll
       for (int it = 0; it < 4; ++it) {
         const int seg = tid + it * NTHREADS;
@@ -635,6 +699,7 @@ __global__ __launch_bounds__(NTHREADS) void gdn_prefill_kernel(PrefillArgs p) {
           *reinterpret_cast<uint4*>(p.out + (cs + c) * out_stride + int64_t(h) * D + 8 * sg) =
               *reinterpret_cast<const uint4*>(sm.O + c * KSTR + 8 * sg);
       }
+      buf ^= 1;
     }
   }
 
