@@ -1,7 +1,14 @@
 // GDN varlen chunked prefill for gfx950 (chunk C = 64, dk = dv = 128).
 //
-// One workgroup of 4 wavefronts walks the chunks of one (sequence, v-head)
-// chain.  The fp32 state never leaves the register file between chunks: wave w
+// One workgroup of 8 wavefronts walks the chunks of one (sequence, v-head)
+// chain as a two-stage pipeline:
+//   * producer waves 4-7 prepare chunk t: stage K and Q in LDS, form the gates,
+//     the masked/decayed products N = strictLower(beta Gamma KK^T) and
+//     P = tril(Gamma QK^T), and T~ = (I + N)^-1;
+//   * consumer waves 0-3 meanwhile advance the state through chunk t-1.
+// Every LDS buffer a consumer reads (K, Q, T~, P, gates) is double-buffered by
+// chunk parity, so a tick is three workgroup barriers with both stages working
+// in between.  The fp32 state never leaves the register file: consumer wave w
 // owns state rows v in [32w, 32w+32) as MFMA accumulators (16x16 tiles of S^T;
 // lane = (k-group g = lane/16, column n = lane%16) holds S[v][k..k+3]).
 //
@@ -17,14 +24,11 @@
 //   o  = scale (e^gamma Q S^T + P v_new)              (:216-234, 273-283)
 //   S  = e^{gamma_last} S + (d v_new)^T K,  d_c = e^{gamma_last - gamma_c}   (:197-202, 286-293)
 //
-// Work split inside a chunk (all waves in parallel between barriers):
-//   A: wave 0 -- the four diagonal 16x16 blocks of N and their inverses (VALU
-//      forward substitution); waves 1, 2 -- the off-diagonal blocks of N (bf16
-//      hi/lo) and P; wave 3 -- two blocks of P and its X = K S^T.
-//   B: wave 3 -- the off-diagonal blocks of T~ by block recursion on MFMA;
-//      waves 0-2 -- their X = K S^T; wave 1 also the next chunk's gates.
-//   C: every wave -- Y, v_new, the output, the state update; the next chunk's
-//      inputs are loaded into registers meanwhile.
+// T~ is built in two steps: each producer wave inverts one diagonal 16x16 block
+// by forward substitution (four lanes per column, partial sums combined across
+// rows with permlane swaps), then one wave forms the off-diagonal blocks by the
+// block recursion X_IJ = -D_I sum_K N_IK X_KJ on MFMA, keeping the X blocks it
+// needs later in registers.
 //
 // Precision: q/k/v are exact bf16 MFMA operands.  Operands that are fp32 values
 // (S, Y, N, T~, d*v_new) are split into bf16 hi + lo pairs so that the products
@@ -52,25 +56,22 @@ typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
 constexpr int C = 64;        // chunk length
 constexpr int D = kHeadDim;  // 128
-constexpr int KSTR = 136;    // bf16 row stride of 128-wide tiles (K, Q, V, O)
+constexpr int KSTR = 136;    // bf16 row stride of 128-wide tiles (K, Q)
 constexpr int TSTR = 72;     // bf16 row stride of 64-wide tiles (T~, P, N)
 constexpr int DSTR = 17;     // fp32 row stride of the diagonal N blocks
-constexpr int NTHREADS = 256;
+constexpr int NTHREADS = 512;
+constexpr int NPROD = 256;   // producer threads (waves 4-7)
 constexpr int kMaxSortedSeqs = 1024;  // longest-first ordering up to this many sequences
 
 struct __align__(16) PrefillSmem {
-  uint16_t K[C * KSTR];       // K chunk [c][perm(k)]
-  uint16_t Q[C * KSTR];       // Q chunk [c][perm(k)]
-  uint16_t V[C * KSTR];       // V chunk [c][v]
-  uint16_t O[C * KSTR];       // output tile [c][v]; sequence lengths at kernel start
-  uint16_t Th[C * TSTR];      // T~ hi [c][perm(j)] (strictly-upper blocks stay 0)
-  uint16_t Tl[C * TSTR];      // T~ lo
-  uint16_t P[C * TSTR];       // P (bf16) [c][perm(j)]
-  uint16_t Nh[C * TSTR];      // off-diagonal blocks of N, hi [i][perm(j)]
+  uint16_t K[2][C * KSTR];    // K chunk [c][perm(k)], by chunk parity
+  uint16_t Q[2][C * KSTR];    // Q chunk [c][perm(k)]
+  uint16_t Th[2][C * TSTR];   // T~ hi [c][perm(j)] (strictly-upper blocks stay 0)
+  uint16_t Tl[2][C * TSTR];   // T~ lo
+  uint16_t P[2][C * TSTR];    // P (bf16) [c][perm(j)] (strictly-upper blocks stay 0)
+  uint16_t Nh[C * TSTR];      // off-diagonal blocks of N, hi [i][perm(j)] (producers only)
   uint16_t Nl[C * TSTR];      // off-diagonal blocks of N, lo
   float Nd[4 * 16 * DSTR];    // diagonal 16x16 blocks of N (fp32)
-  // Per-chunk gate values, double-buffered (chunk parity): the next chunk's are
-  // written while the current chunk's are read.
   float gam[2][C];            // gamma_c (inclusive cumsum of the log gates)
   float bet[2][C];            // beta_c
   float eg[2][C];             // e^{gamma_c}
@@ -105,24 +106,20 @@ __device__ __forceinline__ uint2 read_tr(const uint16_t* p) {
   return __builtin_bit_cast(uint2, v);
 }
 
-// Operand column: column col0 + lane%16 of a row-major tile, contraction rows
-// k0 + kappa(g, s).  In each 16-lane group, lane j reads 4 contiguous columns of
-// row k0 + 4g + j/4 (+16 for the second half); the transpose read hands lane i
-// element i of each of those rows.  PERM: the tile's columns are perm-ordered.
-template <bool PERM>
-__device__ __forceinline__ uint4 frag_tr(const uint16_t* tile, int stride, int k0, int col0, int lane) {
-  const int j = lane & 15, g = lane >> 4;
-  const int col = col0 + 4 * (j & 3);
-  const uint16_t* ptr = tile + (k0 + 4 * g + (j >> 2)) * stride + (PERM ? perm(col) : col);
-  const uint2 a = read_tr(ptr);
-  const uint2 b = read_tr(ptr + 16 * stride);
-  return uint4{a.x, a.y, b.x, b.y};
-}
-
-// Four rows k0 + 4g .. +3 of column col0 + lane%16 (the first half of frag_tr).
+// Four rows k0 + 4g .. +3 of column col0 + lane%16 of a row-major tile whose
+// columns are perm-ordered (groups of 4 columns stay contiguous).  In each
+// 16-lane group, lane j reads 4 contiguous columns of row k0 + 4g + j/4; the
+// transpose read hands lane i element i of each of those rows.
 __device__ __forceinline__ uint2 col4_tr(const uint16_t* tile, int stride, int k0, int col0, int lane) {
   const int j = lane & 15, g = lane >> 4;
-  return read_tr(tile + (k0 + 4 * g + (j >> 2)) * stride + col0 + 4 * (j & 3));
+  return read_tr(tile + (k0 + 4 * g + (j >> 2)) * stride + perm(col0 + 4 * (j & 3)));
+}
+
+// Operand column: column col0 + lane%16, contraction rows k0 + kappa(g, s).
+__device__ __forceinline__ uint4 frag_tr(const uint16_t* tile, int stride, int k0, int col0, int lane) {
+  const uint2 a = col4_tr(tile, stride, k0, col0, lane);
+  const uint2 b = col4_tr(tile, stride, k0 + 16, col0, lane);
+  return uint4{a.x, a.y, b.x, b.y};
 }
 
 // B/A operand (bf16 hi parts) from two accumulator tiles stacked along the
@@ -159,274 +156,20 @@ __device__ __forceinline__ float wave_inclusive_scan(float x, int lane) {
   return x;
 }
 
+// Sum over the four 16-lane rows of a wavefront (lanes j, j+16, j+32, j+48):
+// the row swaps pair rows (0,1), (2,3), then the two halves.
+__device__ __forceinline__ float sum_rows(float x) {
+  const auto a = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  const float y = __uint_as_float(a[0]) + __uint_as_float(a[1]);
+  const auto b = __builtin_amdgcn_permlane32_swap(__float_as_uint(y), __float_as_uint(y), false, false);
+  return __uint_as_float(b[0]) + __uint_as_float(b[1]);
+}
+
 // Orders this wave's LDS writes before its later LDS reads by other lanes.
 __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
-// ---------------------------------------------------------------------------
-// Tiles of N and P from the staged K and Q (16x16 tiles, 4 MFMAs each).
-//   kind 0: diagonal block I of N (fp32, into Nd), from tile K_I K_I^T
-//   kind 1: off-diagonal block (I, J), I > J, of N (bf16 hi/lo), from tile
-//           K_J K_I^T so that a lane holds 4 consecutive columns of one row
-//   kind 2: block (I, J), J <= I, of P, from tile K_J Q_I^T
-// ---------------------------------------------------------------------------
-struct TileJob {
-  int kind, I, J;
-};
-
-__device__ __forceinline__ void tile_epilogue(PrefillSmem& sm, int buf, const TileJob t, const f32x4& acc, int lane) {
-  const int g = lane >> 4, n16 = lane & 15;
-  const float* gam = sm.gam[buf];
-  const float* bet = sm.bet[buf];
-  if (t.kind == 0) {
-    // acc[i] = k_r . k_c, r = 16I + 4g + i, c = 16I + n16
-    const int c = 16 * t.I + n16;
-    const float gc = gam[c];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int ri = 4 * g + i, r = 16 * t.I + ri;
-      sm.Nd[(t.I * 16 + ri) * DSTR + n16] = ri > n16 ? bet[r] * exp_le0(gam[r] - gc) * acc[i] : 0.f;
-    }
-  } else if (t.kind == 1) {
-    // acc[i] = k_c . k_r, c = 16J + 4g + i, r = 16I + n16  ->  N[r][c]
-    const int r = 16 * t.I + n16;
-    const float gr = gam[r], br = bet[r];
-    f32x4 x;
-#pragma unroll
-    for (int i = 0; i < 4; ++i) x[i] = br * exp_le0(gr - gam[16 * t.J + 4 * g + i]) * acc[i];
-    uint2 hi, lo;
-    split4(x, hi, lo);
-    const int pos = r * TSTR + perm(16 * t.J + 4 * g);
-    *reinterpret_cast<uint2*>(sm.Nh + pos) = hi;
-    *reinterpret_cast<uint2*>(sm.Nl + pos) = lo;
-  } else {
-    // acc[i] = k_j . q_c, j = 16J + 4g + i, c = 16I + n16  ->  P[c][j]
-    const int c = 16 * t.I + n16;
-    const float gc = gam[c];
-    float pv[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int j = 16 * t.J + 4 * g + i;
-      pv[i] = j <= c ? exp_le0(gc - gam[j]) * acc[i] : 0.f;
-    }
-    *reinterpret_cast<uint2*>(sm.P + c * TSTR + perm(16 * t.J + 4 * g)) =
-        uint2{pack_bf16x2(pv[0], pv[1]), pack_bf16x2(pv[2], pv[3])};
-  }
-}
-
-template <int NJ>
-__device__ __forceinline__ void run_tiles(PrefillSmem& sm, int buf, const TileJob (&jobs)[NJ], int lane) {
-  f32x4 acc[NJ];
-#pragma unroll
-  for (int t = 0; t < NJ; ++t) acc[t] = zero4();
-#pragma unroll 1
-  for (int ks = 0; ks < 4; ++ks) {
-#pragma unroll
-    for (int t = 0; t < NJ; ++t) {
-      const TileJob j = jobs[t];
-      const int arow = j.kind == 0 ? 16 * j.I : 16 * j.J;
-      const uint16_t* btile = j.kind == 2 ? sm.Q : sm.K;
-      const int brow = 16 * j.I;
-      acc[t] = mfma(frag(sm.K, KSTR, arow, ks, lane), frag(btile, KSTR, brow, ks, lane), acc[t]);
-    }
-  }
-#pragma unroll
-  for (int t = 0; t < NJ; ++t) tile_epilogue(sm, buf, jobs[t], acc[t], lane);
-}
-
-// ---------------------------------------------------------------------------
-// Diagonal blocks of T~: D_I = (I + N_II)^-1 by forward substitution; lane
-// 16I + j owns column j of block I.  Written to Th/Tl (including the zero
-// upper part and the unit diagonal of each block).  One wavefront.
-// ---------------------------------------------------------------------------
-__device__ __forceinline__ void solve_diagonal(PrefillSmem& sm, int lane) {
-  const int I = lane >> 4, j = lane & 15;
-  const float* nb = sm.Nd + I * 16 * DSTR;
-  float x[16];
-#pragma unroll
-  for (int i = 0; i < 16; ++i) x[i] = (i == j) ? 1.f : 0.f;
-#pragma unroll
-  for (int i = 1; i < 16; ++i) {
-    float acc0 = 0.f, acc1 = 0.f;   // two partial sums halve the dependent FMA chain
-#pragma unroll
-    for (int m = 0; m < i; m += 2) {
-      acc0 += nb[i * DSTR + m] * x[m];
-      if (m + 1 < i) acc1 += nb[i * DSTR + m + 1] * x[m + 1];
-    }
-    if (i > j) x[i] = -(acc0 + acc1);
-    if (i & 1) __builtin_amdgcn_sched_barrier(0);  // bound hoisted LDS reads to ~two rows
-  }
-  const int col = perm(16 * I + j);
-#pragma unroll
-  for (int i = 0; i < 16; ++i) {
-    const uint16_t hi = f32_to_bf16(x[i]);
-    sm.Th[(16 * I + i) * TSTR + col] = hi;
-    sm.Tl[(16 * I + i) * TSTR + col] = f32_to_bf16(x[i] - bf16_to_f32(hi));
-  }
-}
-
-// ---------------------------------------------------------------------------
-// Off-diagonal blocks of T~ (one wavefront, MFMA with hi/lo operands):
-//   X_IJ = -D_I G_IJ,  G_IJ = sum_{K=J}^{I-1} N_IK X_KJ  (X_JJ = D_J)
-// in three dependency levels: (1,0) (2,1) (3,2); (2,0) (3,1); (3,0).
-// A operands: rows of N (Nh/Nl) and of T~ (Th/Tl); B operands: the stacked
-// blocks X_KJ read as columns of Th/Tl, or G from registers.  Halves of a 32-wide
-// contraction block that fall outside K in [J, I-1] are zeroed in B.
-// ---------------------------------------------------------------------------
-__device__ __forceinline__ uint4 keep_halves(uint4 b, bool lo_half, bool hi_half) {
-  if (!lo_half) { b.x = 0u; b.y = 0u; }
-  if (!hi_half) { b.z = 0u; b.w = 0u; }
-  return b;
-}
-
-__device__ __forceinline__ f32x4 g_pass(const PrefillSmem& sm, f32x4 G, int I, int J, int q, bool klo, bool khi,
-                                        int lane) {
-  const uint4 ah = frag(sm.Nh, TSTR, 16 * I, q, lane), al = frag(sm.Nl, TSTR, 16 * I, q, lane);
-  const uint4 bh = keep_halves(frag_tr<true>(sm.Th, TSTR, 32 * q, 16 * J, lane), klo, khi);
-  const uint4 bl = keep_halves(frag_tr<true>(sm.Tl, TSTR, 32 * q, 16 * J, lane), klo, khi);
-  G = mfma(ah, bh, G);
-  G = mfma(ah, bl, G);
-  G = mfma(al, bh, G);
-  return G;
-}
-
-// X_IJ = -D_I G, written to Th/Tl.
-__device__ __forceinline__ void finish_block(PrefillSmem& sm, const f32x4& G, int I, int J, int lane) {
-  uint2 gh, gl;
-  split4(G, gh, gl);
-  const bool odd = I & 1;
-  const uint4 bh = odd ? uint4{0u, 0u, gh.x, gh.y} : uint4{gh.x, gh.y, 0u, 0u};
-  const uint4 bl = odd ? uint4{0u, 0u, gl.x, gl.y} : uint4{gl.x, gl.y, 0u, 0u};
-  const uint4 ah = frag(sm.Th, TSTR, 16 * I, I >> 1, lane), al = frag(sm.Tl, TSTR, 16 * I, I >> 1, lane);
-  f32x4 X = zero4();
-  X = mfma(ah, bh, X);
-  X = mfma(ah, bl, X);
-  X = mfma(al, bh, X);
-  const int g = lane >> 4, col = perm(16 * J + (lane & 15));
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const float x = -X[i];
-    const uint16_t hi = f32_to_bf16(x);
-    sm.Th[(16 * I + 4 * g + i) * TSTR + col] = hi;
-    sm.Tl[(16 * I + 4 * g + i) * TSTR + col] = f32_to_bf16(x - bf16_to_f32(hi));
-  }
-}
-
-__device__ __forceinline__ void solve_offdiagonal(PrefillSmem& sm, int lane) {
-  // level 1
-  const f32x4 g10 = g_pass(sm, zero4(), 1, 0, 0, true, false, lane);
-  const f32x4 g21 = g_pass(sm, zero4(), 2, 1, 0, false, true, lane);
-  const f32x4 g32 = g_pass(sm, zero4(), 3, 2, 1, true, false, lane);
-  finish_block(sm, g10, 1, 0, lane);
-  finish_block(sm, g21, 2, 1, lane);
-  finish_block(sm, g32, 3, 2, lane);
-  wave_lds_sync();
-  // level 2
-  const f32x4 g20 = g_pass(sm, zero4(), 2, 0, 0, true, true, lane);
-  f32x4 g31 = g_pass(sm, zero4(), 3, 1, 0, false, true, lane);
-  g31 = g_pass(sm, g31, 3, 1, 1, true, false, lane);
-  finish_block(sm, g20, 2, 0, lane);
-  finish_block(sm, g31, 3, 1, lane);
-  wave_lds_sync();
-  // level 3
-  f32x4 g30 = g_pass(sm, zero4(), 3, 0, 0, true, true, lane);
-  g30 = g_pass(sm, g30, 3, 0, 1, true, false, lane);
-  finish_block(sm, g30, 3, 0, lane);
-}
-
-// X = K S^T (rows c, cols v: Xk[ct][vt]) for this wave's 32 state rows; S
-// enters as hi/lo B operands.
-__device__ __forceinline__ void retrieve(const PrefillSmem& sm, const f32x4 (&S)[2][8], f32x4 (&Xk)[4][2], int lane) {
-#pragma unroll
-  for (int ct = 0; ct < 4; ++ct)
-#pragma unroll
-    for (int vt = 0; vt < 2; ++vt) Xk[ct][vt] = zero4();
-#pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
-    uint4 Sh[2], Sl[2];
-#pragma unroll
-    for (int vt = 0; vt < 2; ++vt) split_pack(S[vt][2 * ks], S[vt][2 * ks + 1], Sh[vt], Sl[vt]);
-#pragma unroll
-    for (int ct = 0; ct < 4; ++ct) {
-      const uint4 ak = frag(sm.K, KSTR, 16 * ct, ks, lane);
-#pragma unroll
-      for (int vt = 0; vt < 2; ++vt) {
-        Xk[ct][vt] = mfma(ak, Sh[vt], Xk[ct][vt]);
-        Xk[ct][vt] = mfma(ak, Sl[vt], Xk[ct][vt]);
-      }
-    }
-    __builtin_amdgcn_sched_barrier(0);  // bound the number of operand loads in flight
-  }
-}
-
-// (Q S^T)^T (rows v, cols c: Xq[vt][ct]) for this wave's 32 state rows; S enters
-// as the bf16 hi A operand (output-only product).
-__device__ __forceinline__ void inter_term(const PrefillSmem& sm, const f32x4 (&S)[2][8], f32x4 (&Xq)[2][4],
-                                           int lane) {
-#pragma unroll
-  for (int ct = 0; ct < 4; ++ct)
-#pragma unroll
-    for (int vt = 0; vt < 2; ++vt) Xq[vt][ct] = zero4();
-#pragma unroll
-  for (int ks = 0; ks < 4; ++ks) {
-    uint4 Sh[2];
-#pragma unroll
-    for (int vt = 0; vt < 2; ++vt) Sh[vt] = pack_hi(S[vt][2 * ks], S[vt][2 * ks + 1]);
-#pragma unroll
-    for (int ct = 0; ct < 4; ++ct) {
-      const uint4 bq = frag(sm.Q, KSTR, 16 * ct, ks, lane);
-#pragma unroll
-      for (int vt = 0; vt < 2; ++vt) Xq[vt][ct] = mfma(Sh[vt], bq, Xq[vt][ct]);
-    }
-  }
-}
-
-struct Prefetch {
-  uint4 k[4], q[4], v[4];
-};
-
-// This thread's K/Q/V segments of a chunk: segment tid + 256*it is token
-// seg/16, columns 8*(seg%16) .. +7, so 16 consecutive threads read one
-// contiguous 256-byte row.
-__device__ __forceinline__ void prefetch_chunk(const PrefillArgs& p, int64_t cs, int clen, int h, int hq, int hk,
-                                               int tid, Prefetch& f) {
-#pragma unroll
-  for (int it = 0; it < 4; ++it) {
-    const int seg = tid + it * NTHREADS, c = seg >> 4, sg = seg & 15;
-    f.k[it] = f.q[it] = f.v[it] = uint4{0u, 0u, 0u, 0u};
-    if (c < clen) {
-      f.k[it] = *reinterpret_cast<const uint4*>(p.k + ((cs + c) * p.Hk + hk) * D + 8 * sg);
-      f.q[it] = *reinterpret_cast<const uint4*>(p.q + ((cs + c) * p.Hq + hq) * D + 8 * sg);
-      f.v[it] = *reinterpret_cast<const uint4*>(p.v + ((cs + c) * p.Hv + h) * D + 8 * sg);
-    }
-  }
-}
-
-// Per-token gate values of a chunk, one token per lane of a wavefront, into
-// gate buffer `buf`.
-__device__ __forceinline__ void chunk_gates(PrefillSmem& sm, int buf, float a, float b, float A_log, float dt_bias,
-                                            int clen, int lane) {
-  const float lg = lane < clen ? log_gate(A_log, a, dt_bias) : 0.f;
-  const float bt = lane < clen ? sigmoidf_(b) : 0.f;
-  const float gm = wave_inclusive_scan(lg, lane);
-  const float glast = readlane_f(gm, clen - 1);
-  sm.gam[buf][lane] = gm;
-  sm.bet[buf][lane] = bt;
-  sm.eg[buf][lane] = expf(gm);
-  sm.dd[buf][lane] = expf(glast - gm);
-}
-
-__device__ __forceinline__ void load_ab(const PrefillArgs& p, int64_t cs, int clen, int h, int lane, float& a,
-                                        float& b) {
-  a = b = 0.f;
-  if (lane < clen) {
-    const int64_t idx = (cs + lane) * p.Hv + h;
-    a = bf16_to_f32(p.a[idx]);
-    b = bf16_to_f32(p.b[idx]);
-  }
 }
 
 // Workgroup barrier ordering LDS only: waits for this wave's LDS operations,
@@ -436,11 +179,557 @@ __device__ __forceinline__ void lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
+// The parity-selected LDS buffers of one chunk.
+struct ChunkBufs {
+  uint16_t* K;
+  uint16_t* Q;
+  uint16_t* Th;
+  uint16_t* Tl;
+  uint16_t* P;
+  float* gam;
+  float* bet;
+  float* eg;
+  float* dd;
+};
+
+__device__ __forceinline__ ChunkBufs chunk_bufs(PrefillSmem& sm, int b) {
+  return ChunkBufs{sm.K[b], sm.Q[b], sm.Th[b], sm.Tl[b], sm.P[b], sm.gam[b], sm.bet[b], sm.eg[b], sm.dd[b]};
+}
+
+// ---------------------------------------------------------------------------
+// Producer side (waves 4-7)
+// ---------------------------------------------------------------------------
+
+// Tiles of N and P from the staged K and Q (16x16 tiles, 4 MFMAs each).
+//   kind 0: diagonal block I of N (fp32, into Nd), from tile K_I K_I^T
+//   kind 1: off-diagonal block (I, J), I > J, of N (bf16 hi/lo), from tile
+//           K_J K_I^T so that a lane holds 4 consecutive columns of one row
+//   kind 2: block (I, J), J <= I, of P, from tile K_J Q_I^T
+struct TileJob {
+  int kind, I, J;
+};
+
+__device__ __forceinline__ void tile_epilogue(PrefillSmem& sm, const ChunkBufs& cb, const TileJob t, const f32x4& acc,
+                                              int lane) {
+  const int g = lane >> 4, n16 = lane & 15;
+  if (t.kind == 0) {
+    // acc[i] = k_r . k_c, r = 16I + 4g + i, c = 16I + n16
+    const int c = 16 * t.I + n16;
+    const float gc = cb.gam[c];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int ri = 4 * g + i, r = 16 * t.I + ri;
+      sm.Nd[(t.I * 16 + ri) * DSTR + n16] = ri > n16 ? cb.bet[r] * exp_le0(cb.gam[r] - gc) * acc[i] : 0.f;
+    }
+  } else if (t.kind == 1) {
+    // acc[i] = k_c . k_r, c = 16J + 4g + i, r = 16I + n16  ->  N[r][c]
+    const int r = 16 * t.I + n16;
+    const float gr = cb.gam[r], br = cb.bet[r];
+    f32x4 x;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) x[i] = br * exp_le0(gr - cb.gam[16 * t.J + 4 * g + i]) * acc[i];
+    uint2 hi, lo;
+    split4(x, hi, lo);
+    const int pos = r * TSTR + perm(16 * t.J + 4 * g);
+    *reinterpret_cast<uint2*>(sm.Nh + pos) = hi;
+    *reinterpret_cast<uint2*>(sm.Nl + pos) = lo;
+  } else {
+    // acc[i] = k_j . q_c, j = 16J + 4g + i, c = 16I + n16  ->  P[c][j]
+    const int c = 16 * t.I + n16;
+    const float gc = cb.gam[c];
+    float pv[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int j = 16 * t.J + 4 * g + i;
+      pv[i] = j <= c ? exp_le0(gc - cb.gam[j]) * acc[i] : 0.f;
+    }
+    *reinterpret_cast<uint2*>(cb.P + c * TSTR + perm(16 * t.J + 4 * g)) =
+        uint2{pack_bf16x2(pv[0], pv[1]), pack_bf16x2(pv[2], pv[3])};
+  }
+}
+
+template <int NJ>
+__device__ __forceinline__ void run_tiles(PrefillSmem& sm, const ChunkBufs& cb, const TileJob (&jobs)[NJ], int lane) {
+  f32x4 acc[NJ];
+#pragma unroll
+  for (int t = 0; t < NJ; ++t) acc[t] = zero4();
+#pragma unroll 1
+  for (int ks = 0; ks < 4; ++ks) {
+#pragma unroll
+    for (int t = 0; t < NJ; ++t) {
+      const TileJob j = jobs[t];
+      const int arow = j.kind == 0 ? 16 * j.I : 16 * j.J;
+      const uint16_t* btile = j.kind == 2 ? cb.Q : cb.K;
+      acc[t] = mfma(frag(cb.K, KSTR, arow, ks, lane), frag(btile, KSTR, 16 * j.I, ks, lane), acc[t]);
+    }
+  }
+#pragma unroll
+  for (int t = 0; t < NJ; ++t) tile_epilogue(sm, cb, jobs[t], acc[t], lane);
+}
+
+// Diagonal block I of T~: D_I = (I + N_II)^-1 by forward substitution, written
+// to Th/Tl (unit diagonal and zero upper part included).  One wavefront: lane
+// (r, j) = (lane/16, lane%16) follows column j and sums the terms m = 4q + r of
+// each row; the four partial sums are combined across rows.
+__device__ __forceinline__ void solve_diagonal_block(const PrefillSmem& sm, const ChunkBufs& cb, int I, int lane) {
+  const int r = lane >> 4, j = lane & 15;
+  const float* nb = sm.Nd + I * 16 * DSTR;
+  float xr[4];  // xr[q] = x[4q + r], x = column j of D_I
+#pragma unroll
+  for (int q = 0; q < 4; ++q) xr[q] = (4 * q + r == j) ? 1.f : 0.f;
+#pragma unroll
+  for (int i = 1; i < 16; ++i) {
+    // x_i = -sum_{m < i} N[i][m] x_m below the diagonal; N[i][m] = 0 for m >= i
+    // (stored zeros), so whole groups of four terms may be summed.
+    float part = 0.f;
+#pragma unroll
+    for (int q = 0; q < (i + 3) / 4; ++q) part += nb[i * DSTR + 4 * q + r] * xr[q];
+    const float tot = sum_rows(part);
+    const float xi = (i > j) ? -tot : (i == j ? 1.f : 0.f);
+    if (r == (i & 3)) xr[i >> 2] = xi;
+  }
+  const int col = perm(16 * I + j);
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int row = 16 * I + 4 * q + r;
+    const uint16_t hi = f32_to_bf16(xr[q]);
+    cb.Th[row * TSTR + col] = hi;
+    cb.Tl[row * TSTR + col] = f32_to_bf16(xr[q] - bf16_to_f32(hi));
+  }
+}
+
+// B operand (hi/lo) from an fp32 accumulator tile placed in one half of a
+// 32-wide contraction block, the other half zero.
+__device__ __forceinline__ void acc_to_b(const f32x4& t, bool upper_half, uint4& bh, uint4& bl) {
+  uint2 h, l;
+  split4(t, h, l);
+  bh = upper_half ? uint4{0u, 0u, h.x, h.y} : uint4{h.x, h.y, 0u, 0u};
+  bl = upper_half ? uint4{0u, 0u, l.x, l.y} : uint4{l.x, l.y, 0u, 0u};
+}
+
+// B operand (hi/lo) of the diagonal block D_J, read from Th/Tl, in its half of
+// contraction block J/2, the other half zero.
+__device__ __forceinline__ void diag_to_b(const ChunkBufs& cb, int J, uint4& bh, uint4& bl, int lane) {
+  const uint2 h = col4_tr(cb.Th, TSTR, 16 * J, 16 * J, lane);
+  const uint2 l = col4_tr(cb.Tl, TSTR, 16 * J, 16 * J, lane);
+  const bool upper = J & 1;
+  bh = upper ? uint4{0u, 0u, h.x, h.y} : uint4{h.x, h.y, 0u, 0u};
+  bl = upper ? uint4{0u, 0u, l.x, l.y} : uint4{l.x, l.y, 0u, 0u};
+}
+
+// Combine two operands that occupy disjoint halves of a contraction block.
+__device__ __forceinline__ uint4 or4(const uint4& a, const uint4& b) {
+  return uint4{a.x | b.x, a.y | b.y, a.z | b.z, a.w | b.w};
+}
+
+// Row block I of a hi/lo tile pair over contraction block q, as A operands.
+struct OpPair {
+  uint4 h, l;
+};
+__device__ __forceinline__ OpPair rows_of(const uint16_t* th, const uint16_t* tl, int I, int q, int lane) {
+  return OpPair{frag(th, TSTR, 16 * I, q, lane), frag(tl, TSTR, 16 * I, q, lane)};
+}
+
+// acc += A * B with A and B given as hi/lo pairs (three passes).
+__device__ __forceinline__ f32x4 mul3(f32x4 acc, const OpPair& a, const uint4& bh, const uint4& bl) {
+  acc = mfma(a.h, bh, acc);
+  acc = mfma(a.h, bl, acc);
+  acc = mfma(a.l, bh, acc);
+  return acc;
+}
+
+// X_IJ = -D_I G; written to Th/Tl and returned.  dI: row block I of T~ over
+// contraction block I/2 with the half that is not D_I masked off.
+__device__ __forceinline__ f32x4 finish_block(const ChunkBufs& cb, const f32x4& G, const OpPair& dI, int I, int J,
+                                              int lane) {
+  uint4 bh, bl;
+  acc_to_b(G, I & 1, bh, bl);
+  const f32x4 X = -mul3(zero4(), dI, bh, bl);
+  const int g = lane >> 4, col = perm(16 * J + (lane & 15));
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    const uint16_t hi = f32_to_bf16(X[i]);
+    cb.Th[(16 * I + 4 * g + i) * TSTR + col] = hi;
+    cb.Tl[(16 * I + 4 * g + i) * TSTR + col] = f32_to_bf16(X[i] - bf16_to_f32(hi));
+  }
+  return X;
+}
+
+// Off-diagonal blocks of T~ (one wavefront):
+//   X_IJ = -D_I G_IJ,  G_IJ = sum_{K=J}^{I-1} N_IK X_KJ  (X_JJ = D_J)
+// Level 1: (1,0) (2,1) (3,2); level 2: (2,0) (3,1); level 3: (3,0).  Every LDS
+// operand is read before the first block store (the stores would otherwise
+// order the later reads behind them); the X blocks of earlier levels stay in
+// registers.
+__device__ __forceinline__ void solve_offdiagonal(const PrefillSmem& sm, const ChunkBufs& cb, int lane) {
+  uint4 d0h, d0l, d1h, d1l, d2h, d2l;
+  diag_to_b(cb, 0, d0h, d0l, lane);
+  diag_to_b(cb, 1, d1h, d1l, lane);
+  diag_to_b(cb, 2, d2h, d2l, lane);
+  // Row blocks of N: (1 | q0) = [N10 0], (2 | q0) = [N20 N21], (3 | q0) = [N30 N31], (3 | q1) = [N32 0].
+  const OpPair n1 = rows_of(sm.Nh, sm.Nl, 1, 0, lane);
+  const OpPair n2 = rows_of(sm.Nh, sm.Nl, 2, 0, lane);
+  const OpPair n30 = rows_of(sm.Nh, sm.Nl, 3, 0, lane);
+  const OpPair n31 = rows_of(sm.Nh, sm.Nl, 3, 1, lane);
+  // D_I as A operands; the other half of the contraction block may hold an
+  // earlier chunk's off-diagonal block and is masked off.
+  OpPair a1 = rows_of(cb.Th, cb.Tl, 1, 0, lane);
+  OpPair a2 = rows_of(cb.Th, cb.Tl, 2, 1, lane);
+  OpPair a3 = rows_of(cb.Th, cb.Tl, 3, 1, lane);
+  a1.h.x = a1.h.y = a1.l.x = a1.l.y = 0u;
+  a2.h.z = a2.h.w = a2.l.z = a2.l.w = 0u;
+  a3.h.x = a3.h.y = a3.l.x = a3.l.y = 0u;
+  // level 1
+  const f32x4 g10 = mul3(zero4(), n1, d0h, d0l);
+  const f32x4 g21 = mul3(zero4(), n2, d1h, d1l);
+  const f32x4 g32 = mul3(zero4(), n31, d2h, d2l);
+  const f32x4 x10 = finish_block(cb, g10, a1, 1, 0, lane);
+  const f32x4 x21 = finish_block(cb, g21, a2, 2, 1, lane);
+  finish_block(cb, g32, a3, 3, 2, lane);
+  // level 2
+  uint4 x10h, x10l, x21h, x21l;
+  acc_to_b(x10, true, x10h, x10l);   // row block 1: upper half of contraction block 0
+  acc_to_b(x21, false, x21h, x21l);  // row block 2: lower half of contraction block 1
+  const uint4 c0h = or4(d0h, x10h), c0l = or4(d0l, x10l);  // column block 0, rows 0-31
+  const f32x4 g20 = mul3(zero4(), n2, c0h, c0l);
+  const f32x4 g31 = mul3(mul3(zero4(), n30, d1h, d1l), n31, x21h, x21l);
+  const f32x4 x20 = finish_block(cb, g20, a2, 2, 0, lane);
+  finish_block(cb, g31, a3, 3, 1, lane);
+  // level 3
+  uint4 x20h, x20l;
+  acc_to_b(x20, false, x20h, x20l);
+  const f32x4 g30 = mul3(mul3(zero4(), n30, c0h, c0l), n31, x20h, x20l);
+  finish_block(cb, g30, a3, 3, 0, lane);
+}
+
+struct ProducerPrefetch {
+  uint4 k[4], q[4];
+  uint16_t a, b;  // raw gate inputs of token pt (first producer wave only)
+};
+
+// Producer thread pt's K/Q segments of a chunk: segment pt + 256*it is token
+// seg/16, columns 8*(seg%16) .. +7 (16 consecutive threads read one 256-byte row).
+__device__ __forceinline__ void producer_prefetch(const PrefillArgs& p, int64_t cs, int clen, int h, int hq, int hk,
+                                                  int pt, ProducerPrefetch& f) {
+#pragma unroll
+  for (int it = 0; it < 4; ++it) {
+    const int seg = pt + it * NPROD, c = seg >> 4, sg = seg & 15;
+    f.k[it] = f.q[it] = uint4{0u, 0u, 0u, 0u};
+    if (c < clen) {
+      f.k[it] = *reinterpret_cast<const uint4*>(p.k + ((cs + c) * p.Hk + hk) * D + 8 * sg);
+      f.q[it] = *reinterpret_cast<const uint4*>(p.q + ((cs + c) * p.Hq + hq) * D + 8 * sg);
+    }
+  }
+  if (pt < 64) {  // wave-uniform; the row index is clamped and padding masked when used
+    const int64_t idx = (cs + (pt < clen ? pt : clen - 1)) * p.Hv + h;
+    f.a = p.a[idx];
+    f.b = p.b[idx];
+  }
+}
+
+// The producer loop: tick t prepares chunk t into the buffers of parity t & 1.
+// Three barriers per tick, matching the consumer loop.
+__device__ __forceinline__ void producer_loop(PrefillSmem& sm, const PrefillArgs& p, int64_t s0, int64_t s1,
+                                              int nchunks, int h, int hq, int hk, int pw, int lane0) {
+  const int pt = pw * 64 + lane0;
+  const float A_log = p.A_log[h];
+  const float dt_bias = p.dt_bias[h];
+  ProducerPrefetch f;
+  producer_prefetch(p, s0, int(s1 - s0 < C ? s1 - s0 : C), h, hq, hk, pt, f);
+  lds_barrier();  // LDS clearing done (matched by the consumers)
+
+  for (int t = 0; t <= nchunks; ++t) {
+    // The lane index is re-materialised opaquely each tick so that lane-dependent
+    // LDS addresses are recomputed in the loop rather than hoisted and spilled.
+    int lane = lane0;
+    asm volatile("" : "+v"(lane));
+    const bool work = t < nchunks;
+    const int64_t cs = s0 + int64_t(t) * C;
+    const int clen = work ? int(s1 - cs < C ? s1 - cs : C) : 0;
+    const ChunkBufs cb = chunk_bufs(sm, t & 1);
+
+    // 1: stage K/Q (permuted columns), gates
+    if (work) {
+#pragma unroll
+      for (int it = 0; it < 4; ++it) {
+        const int seg = pt + it * NPROD, c = seg >> 4, sg = seg & 15;
+        const int col0 = (8 * sg) & ~31, r0 = (8 * sg) & 31;
+        const int pa = c * KSTR + col0 + perm32(r0), pb = c * KSTR + col0 + perm32(r0 + 4);
+        *reinterpret_cast<uint2*>(cb.K + pa) = uint2{f.k[it].x, f.k[it].y};
+        *reinterpret_cast<uint2*>(cb.K + pb) = uint2{f.k[it].z, f.k[it].w};
+        *reinterpret_cast<uint2*>(cb.Q + pa) = uint2{f.q[it].x, f.q[it].y};
+        *reinterpret_cast<uint2*>(cb.Q + pb) = uint2{f.q[it].z, f.q[it].w};
+      }
+      if (pw == 0) {
+        const float lg = lane < clen ? log_gate(A_log, bf16_to_f32(f.a), dt_bias) : 0.f;
+        const float bt = lane < clen ? sigmoidf_(bf16_to_f32(f.b)) : 0.f;
+        const float gm = wave_inclusive_scan(lg, lane);
+        const float glast = readlane_f(gm, clen - 1);
+        cb.gam[lane] = gm;
+        cb.bet[lane] = bt;
+        cb.eg[lane] = expf(gm);
+        cb.dd[lane] = expf(glast - gm);
+      }
+    }
+    lds_barrier();
+
+    // 2: N tiles (and two P tiles), diagonal blocks of T~
+    if (work) {
+      switch (pw) {
+        case 0: {
+          const TileJob jobs[3] = {{0, 0, 0}, {1, 1, 0}, {1, 2, 0}};
+          run_tiles(sm, cb, jobs, lane);
+          break;
+        }
+        case 1: {
+          const TileJob jobs[3] = {{0, 1, 1}, {1, 3, 0}, {1, 2, 1}};
+          run_tiles(sm, cb, jobs, lane);
+          break;
+        }
+        case 2: {
+          const TileJob jobs[3] = {{0, 2, 2}, {1, 3, 1}, {1, 3, 2}};
+          run_tiles(sm, cb, jobs, lane);
+          break;
+        }
+        default: {
+          const TileJob jobs[3] = {{0, 3, 3}, {2, 3, 3}, {2, 3, 2}};
+          run_tiles(sm, cb, jobs, lane);
+          break;
+        }
+      }
+      wave_lds_sync();  // this wave wrote its diagonal block of N
+      solve_diagonal_block(sm, cb, pw, lane);
+    }
+    lds_barrier();
+
+    // 3: off-diagonal blocks of T~ (last producer wave), remaining P tiles;
+    // next chunk's inputs into registers
+    if (work) {
+      switch (pw) {
+        case 0: {
+          const TileJob jobs[3] = {{2, 0, 0}, {2, 1, 0}, {2, 1, 1}};
+          run_tiles(sm, cb, jobs, lane);
+          break;
+        }
+        case 1: {
+          const TileJob jobs[3] = {{2, 2, 0}, {2, 2, 1}, {2, 2, 2}};
+          run_tiles(sm, cb, jobs, lane);
+          break;
+        }
+        case 2: {
+          const TileJob jobs[2] = {{2, 3, 0}, {2, 3, 1}};
+          run_tiles(sm, cb, jobs, lane);
+          break;
+        }
+        default:
+          solve_offdiagonal(sm, cb, lane);
+          break;
+      }
+      const int64_t ncs = cs + C;
+      if (ncs < s1) producer_prefetch(p, ncs, int(s1 - ncs < C ? s1 - ncs : C), h, hq, hk, pt, f);
+    }
+    lds_barrier();
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Consumer side (waves 0-3; wave w owns state rows 32w .. 32w+31)
+// ---------------------------------------------------------------------------
+
+// Xk = K S^T (rows c, cols v) with S as hi/lo B operands, and Xq = (Q S^T)^T
+// (rows v, cols c) with S's hi part as the A operand (output-only product).
+__device__ __forceinline__ void retrieve(const ChunkBufs& cb, const f32x4 (&S)[2][8], f32x4 (&Xk)[4][2],
+                                         f32x4 (&Xq)[2][4], int lane) {
+#pragma unroll
+  for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+    for (int vt = 0; vt < 2; ++vt) Xk[ct][vt] = Xq[vt][ct] = zero4();
+#pragma unroll
+  for (int ks = 0; ks < 4; ++ks) {
+    uint4 Sh[2], Sl[2];
+#pragma unroll
+    for (int vt = 0; vt < 2; ++vt) split_pack(S[vt][2 * ks], S[vt][2 * ks + 1], Sh[vt], Sl[vt]);
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) {
+      const uint4 ak = frag(cb.K, KSTR, 16 * ct, ks, lane);
+      const uint4 bq = frag(cb.Q, KSTR, 16 * ct, ks, lane);
+#pragma unroll
+      for (int vt = 0; vt < 2; ++vt) {
+        Xk[ct][vt] = mfma(ak, Sh[vt], Xk[ct][vt]);
+        Xk[ct][vt] = mfma(ak, Sl[vt], Xk[ct][vt]);
+        Xq[vt][ct] = mfma(Sh[vt], bq, Xq[vt][ct]);
+      }
+    }
+    __builtin_amdgcn_sched_barrier(0);  // bound the number of operand loads in flight
+  }
+}
+
+// V[c][v] for c = 16ct + 4g + i, v = 32w + 16vt + n16 of the chunk at cs, as raw
+// bf16 bits.  Rows past the chunk end load the last row (in bounds) and are
+// masked when used, so the loads need no branches and can stay in flight.
+__device__ __forceinline__ void load_v(const PrefillArgs& p, int64_t cs, int clen, int h, int wave, int lane,
+                                       uint16_t (&vr)[4][2][4]) {
+  const int64_t vstride = int64_t(p.Hv) * D;
+  const uint16_t* base = p.v + cs * vstride + int64_t(h) * D + 32 * wave + (lane & 15);
+  const int g = lane >> 4;
+#pragma unroll
+  for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int c = 16 * ct + 4 * g + i;
+      const int64_t row = c < clen ? c : clen - 1;
+#pragma unroll
+      for (int vt = 0; vt < 2; ++vt) vr[ct][vt][i] = base[row * vstride + 16 * vt];
+    }
+}
+
+__device__ __forceinline__ void pack_v(const uint16_t (&vr)[4][2][4], uint32_t (&vbits)[4][2][2]) {
+#pragma unroll
+  for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+    for (int vt = 0; vt < 2; ++vt) {
+      vbits[ct][vt][0] = uint32_t(vr[ct][vt][0]) | (uint32_t(vr[ct][vt][1]) << 16);
+      vbits[ct][vt][1] = uint32_t(vr[ct][vt][2]) | (uint32_t(vr[ct][vt][3]) << 16);
+    }
+}
+
+// The consumer loop: tick t (>= 1) advances the state through chunk t-1 from the
+// buffers of parity (t-1) & 1.  Three barriers per tick, matching the producers.
+__device__ __forceinline__ void consumer_loop(PrefillSmem& sm, const PrefillArgs& p, int64_t s0, int64_t s1,
+                                              int nchunks, int h, int wave, int lane0, f32x4 (&S)[2][8]) {
+  lds_barrier();  // LDS clearing done (matched by the producers)
+  // Tick 0 only fills the pipeline.
+  lds_barrier();
+  lds_barrier();
+  lds_barrier();
+  const int64_t vstride = int64_t(p.Hv) * D;
+  // V of the chunk processed next, loaded a tick ahead and packed in pairs of rows.
+  uint16_t vr[4][2][4];
+  uint32_t vbits[4][2][2];
+  load_v(p, s0, int(s1 - s0 < C ? s1 - s0 : C), h, wave, lane0, vr);
+  pack_v(vr, vbits);
+  for (int t = 1; t <= nchunks; ++t) {
+    int lane = lane0;
+    asm volatile("" : "+v"(lane));
+    const int g = lane >> 4, n16 = lane & 15;
+    const int64_t cs = s0 + int64_t(t - 1) * C;
+    const int clen = int(s1 - cs < C ? s1 - cs : C);
+    const ChunkBufs cb = chunk_bufs(sm, (t - 1) & 1);
+
+    // 1: X = K S^T, (Q S^T)^T
+    f32x4 Xk[4][2], Xq[2][4];
+    retrieve(cb, S, Xk, Xq, lane);
+    lds_barrier();
+
+    // 2: Y, v_new, output
+    // Y = beta (V - e^gamma X); element (c = 16ct + 4g + i, v = 32w + 16vt + n16).
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) {
+      const float4 bc = *reinterpret_cast<const float4*>(cb.bet + 16 * ct + 4 * g);
+      const float4 ec = *reinterpret_cast<const float4*>(cb.eg + 16 * ct + 4 * g);
+      const float b4[4] = {bc.x, bc.y, bc.z, bc.w}, e4[4] = {ec.x, ec.y, ec.z, ec.w};
+#pragma unroll
+      for (int vt = 0; vt < 2; ++vt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+          const uint32_t w = vbits[ct][vt][i >> 1];
+          const float vf = 16 * ct + 4 * g + i < clen ? ((i & 1) ? bf16hi_f32(w) : bf16lo_f32(w)) : 0.f;
+          Xk[ct][vt][i] = b4[i] * (vf - e4[i] * Xk[ct][vt][i]);
+        }
+      const float ecn = cb.eg[16 * ct + n16];  // e^gamma of output column c = 16ct + n16
+#pragma unroll
+      for (int vt = 0; vt < 2; ++vt) Xq[vt][ct] = Xq[vt][ct] * ecn;
+    }
+    // v_new = T~ Y (contraction over the rows of Y in blocks js; T~ is lower triangular).
+    uint4 Yh[2][2], Yl[2][2];
+#pragma unroll
+    for (int vt = 0; vt < 2; ++vt)
+#pragma unroll
+      for (int js = 0; js < 2; ++js) split_pack(Xk[2 * js][vt], Xk[2 * js + 1][vt], Yh[vt][js], Yl[vt][js]);
+    f32x4 Vn[4][2];
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) {
+#pragma unroll
+      for (int vt = 0; vt < 2; ++vt) Vn[ct][vt] = zero4();
+#pragma unroll
+      for (int js = 0; js <= (ct >> 1); ++js) {
+        const uint4 th = frag(cb.Th, TSTR, 16 * ct, js, lane);
+        const uint4 tl = frag(cb.Tl, TSTR, 16 * ct, js, lane);
+#pragma unroll
+        for (int vt = 0; vt < 2; ++vt) {
+          Vn[ct][vt] = mfma(th, Yh[vt][js], Vn[ct][vt]);
+          Vn[ct][vt] = mfma(th, Yl[vt][js], Vn[ct][vt]);
+          Vn[ct][vt] = mfma(tl, Yh[vt][js], Vn[ct][vt]);
+        }
+      }
+    }
+    // o^T = e^gamma (S Q^T) + v_new^T P^T (rows v, cols c); P is lower triangular.
+#pragma unroll
+    for (int js = 0; js < 2; ++js) {
+      uint4 vb[2];
+#pragma unroll
+      for (int vt = 0; vt < 2; ++vt) vb[vt] = pack_hi(Vn[2 * js][vt], Vn[2 * js + 1][vt]);
+#pragma unroll
+      for (int ct = 2 * js; ct < 4; ++ct) {
+        const uint4 pq = frag(cb.P, TSTR, 16 * ct, js, lane);
+#pragma unroll
+        for (int vt = 0; vt < 2; ++vt) Xq[vt][ct] = mfma(vb[vt], pq, Xq[vt][ct]);
+      }
+    }
+    // Lane holds o[c = 16ct + n16][v = 32w + 16vt + 4g .. +3]: one 8-byte store each.
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) {
+      const int c = 16 * ct + n16;
+      if (c < clen) {
+#pragma unroll
+        for (int vt = 0; vt < 2; ++vt) {
+          const f32x4 o = Xq[vt][ct] * p.scale;
+          *reinterpret_cast<uint2*>(p.out + (cs + c) * vstride + int64_t(h) * D + 32 * wave + 16 * vt + 4 * g) =
+              uint2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
+        }
+      }
+    }
+    lds_barrier();
+
+    // 3: S = e^{gamma_last} S + sum_c K[c]^T (d_c v_new[c]),  d_c = e^{gamma_last - gamma_c}
+    if (t < nchunks) {
+      const int64_t ncs = cs + C;
+      load_v(p, ncs, int(s1 - ncs < C ? s1 - ncs : C), h, wave, lane, vr);
+    }
+    const float dlast = cb.eg[clen - 1];
+    uint4 Uh[2][2], Ul[2][2];
+#pragma unroll
+    for (int js = 0; js < 2; ++js) {
+      const float4 d0 = *reinterpret_cast<const float4*>(cb.dd + 32 * js + 4 * g);
+      const float4 d1 = *reinterpret_cast<const float4*>(cb.dd + 32 * js + 16 + 4 * g);
+      const f32x4 e0 = {d0.x, d0.y, d0.z, d0.w}, e1 = {d1.x, d1.y, d1.z, d1.w};
+#pragma unroll
+      for (int vt = 0; vt < 2; ++vt) split_pack(Vn[2 * js][vt] * e0, Vn[2 * js + 1][vt] * e1, Uh[vt][js], Ul[vt][js]);
+    }
+#pragma unroll
+    for (int kt = 0; kt < 8; ++kt) {
+#pragma unroll
+      for (int vt = 0; vt < 2; ++vt) S[vt][kt] = S[vt][kt] * dlast;
+#pragma unroll
+      for (int js = 0; js < 2; ++js) {
+        const uint4 ak = frag_tr(cb.K, KSTR, 32 * js, 16 * kt, lane);
+#pragma unroll
+        for (int vt = 0; vt < 2; ++vt) {
+          S[vt][kt] = mfma(ak, Uh[vt][js], S[vt][kt]);
+          S[vt][kt] = mfma(ak, Ul[vt][js], S[vt][kt]);
+        }
+      }
+    }
+    if (t < nchunks) pack_v(vr, vbits);
+    lds_barrier();
+  }
+}
+
 // The sequence of rank `rank` in descending length order (ties: lower index
 // first), so the longest chains start first; natural order for large batches.
 __device__ int pick_sequence(PrefillSmem& sm, const PrefillArgs& p, int rank, int tid) {
   if (p.N <= 1 || p.N > kMaxSortedSeqs) return rank;
-  int* len = reinterpret_cast<int*>(sm.O);
+  int* len = reinterpret_cast<int*>(sm.Nh);  // scratch until the first chunk
   for (int i = tid; i < p.N; i += NTHREADS) {
     int64_t a = load_cu(p.cu_seqlens, p.cu_is_64, i), b = load_cu(p.cu_seqlens, p.cu_is_64, i + 1);
     a = a < 0 ? 0 : (a > p.T ? p.T : a);
@@ -477,12 +766,34 @@ __global__ __launch_bounds__(NTHREADS) void gdn_prefill_kernel(PrefillArgs p) {
   int64_t s1 = load_cu(p.cu_seqlens, p.cu_is_64, seq + 1);
   s0 = s0 < 0 ? 0 : (s0 > p.T ? p.T : s0);
   s1 = s1 < s0 ? s0 : (s1 > p.T ? p.T : s1);
+  const int nchunks = int((s1 - s0 + C - 1) / C);
 
-  // State slab of this wave: rows v = 32*wave + 16*vt + n16, cols k = 16*kt + 4g + i.
+  if (nchunks > 0) {
+    // Blocks of T~, N and P that are never written per chunk are read as zeros
+    // (strictly-upper blocks, the diagonal blocks of Nh/Nl): clear them once.
+    // pick_sequence's last read of its scratch precedes its final barrier.
+    const uint4 z = uint4{0u, 0u, 0u, 0u};
+    for (int e = tid; e < C * TSTR / 8; e += NTHREADS) {
+      reinterpret_cast<uint4*>(sm.P[0])[e] = z;
+      reinterpret_cast<uint4*>(sm.P[1])[e] = z;
+      reinterpret_cast<uint4*>(sm.Th[0])[e] = z;
+      reinterpret_cast<uint4*>(sm.Th[1])[e] = z;
+      reinterpret_cast<uint4*>(sm.Tl[0])[e] = z;
+      reinterpret_cast<uint4*>(sm.Tl[1])[e] = z;
+      reinterpret_cast<uint4*>(sm.Nh)[e] = z;
+      reinterpret_cast<uint4*>(sm.Nl)[e] = z;
+    }
+  }
+
+  if (wave >= 4) {
+    if (nchunks > 0) producer_loop(sm, p, s0, s1, nchunks, h, hq, hk, wave - 4, lane0);
+    return;
+  }
+
+  // Consumer state slab: rows v = 32*wave + 16*vt + n16, cols k = 16*kt + 4g + i.
   const int64_t state_head = (int64_t(seq) * p.Hv + h) * D * D;
-  f32x4 S[2][8];
-  {
   const int g = lane0 >> 4, n16 = lane0 & 15;
+  f32x4 S[2][8];
 #pragma unroll
   for (int vt = 0; vt < 2; ++vt) {
     const int v = 32 * wave + 16 * vt + n16;
@@ -496,216 +807,10 @@ __global__ __launch_bounds__(NTHREADS) void gdn_prefill_kernel(PrefillArgs p) {
       }
     }
   }
-  }
-
-  if (s1 > s0) {
-    // Blocks of T~, N and P that are never written per chunk are read as zeros
-    // (strictly-upper blocks, the diagonal blocks of Nh/Nl): clear them once.
-    for (int e = tid; e < C * TSTR / 8; e += NTHREADS) {
-      reinterpret_cast<uint4*>(sm.P)[e] = uint4{0u, 0u, 0u, 0u};
-      reinterpret_cast<uint4*>(sm.Th)[e] = uint4{0u, 0u, 0u, 0u};
-      reinterpret_cast<uint4*>(sm.Tl)[e] = uint4{0u, 0u, 0u, 0u};
-      reinterpret_cast<uint4*>(sm.Nh)[e] = uint4{0u, 0u, 0u, 0u};
-      reinterpret_cast<uint4*>(sm.Nl)[e] = uint4{0u, 0u, 0u, 0u};
-    }
-    const float A_log = p.A_log[h];
-    const float dt_bias = p.dt_bias[h];
-    const int64_t out_stride = int64_t(p.Hv) * D;
-
-    Prefetch f;
-    {
-      const int clen0 = int(s1 - s0 < C ? s1 - s0 : C);
-      prefetch_chunk(p, s0, clen0, h, hq, hk, tid, f);
-      if (wave == 1) {
-        float a, b;
-        load_ab(p, s0, clen0, h, lane0, a, b);
-        chunk_gates(sm, 0, a, b, A_log, dt_bias, clen0, lane0);
-      }
-    }
-    int buf = 0;   // gate buffer of the current chunk
-
-    for (int64_t cs = s0; cs < s1; cs += C) {
-      const int clen = int(s1 - cs < C ? s1 - cs : C);
-      // The lane index is re-materialised opaquely each chunk so that the many
-      // lane-dependent LDS addresses below are recomputed in the loop instead of
-      // being hoisted out of it (and spilled).
-      int lane = lane0;
-      asm volatile("" : "+v"(lane));
-      const int g = lane >> 4, n16 = lane & 15;
-      lds_barrier();  // the previous chunk's LDS reads are done
-
-      // ---- stage K, Q, V from the prefetched registers; gates ---------------
-#pragma unroll
-      for (int it = 0; it < 4; ++it) {
-        const int seg = tid + it * NTHREADS, c = seg >> 4, sg = seg & 15;
-        const int col0 = (8 * sg) & ~31, r0 = (8 * sg) & 31;
-        const int pa = col0 + perm32(r0), pb = col0 + perm32(r0 + 4);
-        *reinterpret_cast<uint2*>(sm.K + c * KSTR + pa) = uint2{f.k[it].x, f.k[it].y};
-        *reinterpret_cast<uint2*>(sm.K + c * KSTR + pb) = uint2{f.k[it].z, f.k[it].w};
-        *reinterpret_cast<uint2*>(sm.Q + c * KSTR + pa) = uint2{f.q[it].x, f.q[it].y};
-        *reinterpret_cast<uint2*>(sm.Q + c * KSTR + pb) = uint2{f.q[it].z, f.q[it].w};
-        *reinterpret_cast<uint4*>(sm.V + c * KSTR + 8 * sg) = f.v[it];
-      }
-      lds_barrier();
-      const float* gam = sm.gam[buf];
-      const float* bet = sm.bet[buf];
-      const float* egv = sm.eg[buf];
-      const float* ddv = sm.dd[buf];
-
-      // Next chunk's gate inputs (wave 1): loaded now, turned into gates in phase B.
-      const int64_t nc = cs + C;
-      const int nclen = int(s1 - nc < C ? s1 - nc : C);
-      float na = 0.f, nb = 0.f;
-      if (wave == 1 && nc < s1) load_ab(p, nc, nclen, h, lane, na, nb);
-
-      f32x4 Xk[4][2];
-      // ---- phase A -------------------------------------------------------------
-      if (wave == 0) {
-        const TileJob jobs[4] = {{0, 0, 0}, {0, 1, 1}, {0, 2, 2}, {0, 3, 3}};
-        run_tiles(sm, buf, jobs, lane);
-        wave_lds_sync();
-        solve_diagonal(sm, lane);
-      } else if (wave == 1) {
-        const TileJob jobs[8] = {{1, 1, 0}, {1, 2, 0}, {1, 3, 0}, {1, 2, 1},
-                                 {1, 3, 1}, {1, 3, 2}, {2, 0, 0}, {2, 1, 1}};
-        run_tiles(sm, buf, jobs, lane);
-      } else if (wave == 2) {
-        const TileJob jobs[6] = {{2, 1, 0}, {2, 2, 0}, {2, 2, 1}, {2, 2, 2}, {2, 3, 0}, {2, 3, 1}};
-        run_tiles(sm, buf, jobs, lane);
-      } else {
-        const TileJob jobs[2] = {{2, 3, 2}, {2, 3, 3}};
-        run_tiles(sm, buf, jobs, lane);
-        retrieve(sm, S, Xk, lane);
-      }
-      lds_barrier();
-
-      // ---- phase B -------------------------------------------------------------
-      if (wave == 3) {
-        solve_offdiagonal(sm, lane);
-      } else {
-        retrieve(sm, S, Xk, lane);
-        // Next chunk's gates, into the other gate buffer.
-        if (wave == 1 && nc < s1) chunk_gates(sm, buf ^ 1, na, nb, A_log, dt_bias, nclen, lane);
-      }
-      lds_barrier();
-
-      // ---- phase C: Y, v_new, output, state update -------------------------------
-      // Y = beta (V - e^gamma X); element (c = 16ct + 4g + i, v = 32w + 16vt + n16).
-#pragma unroll
-      for (int ct = 0; ct < 4; ++ct) {
-        const float4 bc = *reinterpret_cast<const float4*>(bet + 16 * ct + 4 * g);
-        const float4 ec = *reinterpret_cast<const float4*>(egv + 16 * ct + 4 * g);
-        const float b4[4] = {bc.x, bc.y, bc.z, bc.w}, e4[4] = {ec.x, ec.y, ec.z, ec.w};
-#pragma unroll
-        for (int vt = 0; vt < 2; ++vt) {
-          const uint2 vv = col4_tr(sm.V, KSTR, 16 * ct, 32 * wave + 16 * vt, lane);
-          const float vf[4] = {bf16lo_f32(vv.x), bf16hi_f32(vv.x), bf16lo_f32(vv.y), bf16hi_f32(vv.y)};
-#pragma unroll
-          for (int i = 0; i < 4; ++i) Xk[ct][vt][i] = b4[i] * (vf[i] - e4[i] * Xk[ct][vt][i]);
-        }
-      }
-
-      // v_new = T~ Y (contraction over the rows of Y: blocks js; T~ is lower triangular).
-      uint4 Yh[2][2], Yl[2][2];
-#pragma unroll
-      for (int vt = 0; vt < 2; ++vt)
-#pragma unroll
-        for (int js = 0; js < 2; ++js) split_pack(Xk[2 * js][vt], Xk[2 * js + 1][vt], Yh[vt][js], Yl[vt][js]);
-      f32x4 Vn[4][2];
-#pragma unroll
-      for (int ct = 0; ct < 4; ++ct) {
-#pragma unroll
-        for (int vt = 0; vt < 2; ++vt) Vn[ct][vt] = zero4();
-#pragma unroll
-        for (int js = 0; js <= (ct >> 1); ++js) {
-          const uint4 th = frag(sm.Th, TSTR, 16 * ct, js, lane);
-          const uint4 tl = frag(sm.Tl, TSTR, 16 * ct, js, lane);
-#pragma unroll
-          for (int vt = 0; vt < 2; ++vt) {
-            Vn[ct][vt] = mfma(th, Yh[vt][js], Vn[ct][vt]);
-            Vn[ct][vt] = mfma(th, Yl[vt][js], Vn[ct][vt]);
-            Vn[ct][vt] = mfma(tl, Yh[vt][js], Vn[ct][vt]);
-          }
-        }
-      }
-
-      // o^T = e^gamma (S Q^T) + v_new^T P^T (rows v, cols c); P is lower triangular.
-      f32x4 Xq[2][4];
-      inter_term(sm, S, Xq, lane);
-#pragma unroll
-      for (int ct = 0; ct < 4; ++ct) {
-        const float ecn = egv[16 * ct + n16];   // e^gamma of column c = 16ct + n16
-#pragma unroll
-        for (int vt = 0; vt < 2; ++vt) Xq[vt][ct] = Xq[vt][ct] * ecn;
-      }
-#pragma unroll
-      for (int js = 0; js < 2; ++js) {
-        uint4 vb[2];
-#pragma unroll
-        for (int vt = 0; vt < 2; ++vt) vb[vt] = pack_hi(Vn[2 * js][vt], Vn[2 * js + 1][vt]);
-#pragma unroll
-        for (int ct = 2 * js; ct < 4; ++ct) {
-          const uint4 pb = frag(sm.P, TSTR, 16 * ct, js, lane);
-#pragma unroll
-          for (int vt = 0; vt < 2; ++vt) Xq[vt][ct] = mfma(vb[vt], pb, Xq[vt][ct]);
-        }
-      }
-      // Lane holds o[c = 16ct + n16][v = 32w + 16vt + 4g .. +3]: one 8-byte LDS write each.
-#pragma unroll
-      for (int ct = 0; ct < 4; ++ct) {
-        const int c = 16 * ct + n16;
-#pragma unroll
-        for (int vt = 0; vt < 2; ++vt) {
-          const f32x4 o = Xq[vt][ct] * p.scale;
-          *reinterpret_cast<uint2*>(sm.O + c * KSTR + 32 * wave + 16 * vt + 4 * g) =
-              uint2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
-        }
-      }
-
-      // S = e^{gamma_last} S + sum_c K[c]^T (d_c v_new[c]),  d_c = e^{gamma_last - gamma_c}
-      const float dlast = egv[clen - 1];
-      uint4 Uh[2][2], Ul[2][2];
-#pragma unroll
-      for (int js = 0; js < 2; ++js) {
-        const float4 d0 = *reinterpret_cast<const float4*>(ddv + 32 * js + 4 * g);
-        const float4 d1 = *reinterpret_cast<const float4*>(ddv + 32 * js + 16 + 4 * g);
-        const f32x4 e0 = {d0.x, d0.y, d0.z, d0.w}, e1 = {d1.x, d1.y, d1.z, d1.w};
-#pragma unroll
-        for (int vt = 0; vt < 2; ++vt) split_pack(Vn[2 * js][vt] * e0, Vn[2 * js + 1][vt] * e1, Uh[vt][js], Ul[vt][js]);
-      }
-#pragma unroll
-      for (int kt = 0; kt < 8; ++kt) {
-#pragma unroll
-        for (int vt = 0; vt < 2; ++vt) S[vt][kt] = S[vt][kt] * dlast;
-#pragma unroll
-        for (int js = 0; js < 2; ++js) {
-          const uint4 ak = frag_tr<true>(sm.K, KSTR, 32 * js, 16 * kt, lane);
-#pragma unroll
-          for (int vt = 0; vt < 2; ++vt) {
-            S[vt][kt] = mfma(ak, Uh[vt][js], S[vt][kt]);
-            S[vt][kt] = mfma(ak, Ul[vt][js], S[vt][kt]);
-          }
-        }
-      }
-
-      lds_barrier();  // output tile complete
-      // Next chunk's K/Q/V, in flight during the output store and the barrier.
-      if (nc < s1) prefetch_chunk(p, nc, nclen, h, hq, hk, tid, f);
-#pragma unroll
-      for (int it = 0; it < 4; ++it) {
-        const int seg = tid + it * NTHREADS;
-        const int c = seg >> 4, sg = seg & 15;
-        if (c < clen)
-          *reinterpret_cast<uint4*>(p.out + (cs + c) * out_stride + int64_t(h) * D + 8 * sg) =
-              *reinterpret_cast<const uint4*>(sm.O + c * KSTR + 8 * sg);
-      }
-      buf ^= 1;
-    }
-  }
+  if (nchunks > 0) consumer_loop(sm, p, s0, s1, nchunks, h, wave, lane0, S);
 
   // Final state (for an empty sequence: the initial state, or zeros).
-  if (s1 > s0 || p.state != p.new_state) {
-    const int g = lane0 >> 4, n16 = lane0 & 15;
+  if (nchunks > 0 || p.state != p.new_state) {
 #pragma unroll
     for (int vt = 0; vt < 2; ++vt) {
       const int v = 32 * wave + 16 * vt + n16;
