@@ -16,7 +16,7 @@
 // log-gate 0, as kernel_prefill.cu:102-114, 125-132 pads them):
 //   gamma = inclusive cumsum of the log gates, beta = sigmoid(b)   (a1, :101-122)
 //   N[i][j] = beta_i e^{gamma_i - gamma_j} k_i.k_j   (i > j)       (:134-146, sign folded)
-//   P[i][j] = e^{gamma_i - gamma_j} q_i.k_j          (j <= i)       (:165-185)
+//   P[i][j] = e^{gamma_i - gamma_j} q_i.k_j          (j <= i)       (:165-185; stored times scale)
 //   T~ = (I + N)^-1                                   (:148-163)
 //   X  = K S^T                                        (retrieval from the chunk-start state)
 //   Y  = beta (V - e^gamma X)
@@ -56,11 +56,13 @@ typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
 constexpr int C = 64;        // chunk length
 constexpr int D = kHeadDim;  // 128
-constexpr int KSTR = 136;    // bf16 row stride of 128-wide tiles (K, Q)
+constexpr int KSTR = 128;    // bf16 row stride of the K and Q tiles (16-byte slots XOR-swizzled by row)
+constexpr int VSTR = 144;    // bf16 row stride of the V tile (rows 32 bytes apart modulo 128)
 constexpr int TSTR = 72;     // bf16 row stride of 64-wide tiles (T~, P, N)
-constexpr int DSTR = 17;     // fp32 row stride of the diagonal N blocks
+constexpr int DSTR = 20;     // fp32 row stride of the diagonal N blocks (16-byte aligned rows)
 constexpr int NTHREADS = 512;
 constexpr int NPROD = 256;   // producer threads (waves 4-7)
+constexpr int NROWS = C - 16;  // rows of N kept for the off-diagonal solve
 constexpr int kMaxSortedSeqs = 1024;  // longest-first ordering up to this many sequences
 
 struct __align__(16) PrefillSmem {
@@ -69,8 +71,9 @@ struct __align__(16) PrefillSmem {
   uint16_t Th[2][C * TSTR];   // T~ hi [c][perm(j)] (strictly-upper blocks stay 0)
   uint16_t Tl[2][C * TSTR];   // T~ lo
   uint16_t P[2][C * TSTR];    // P (bf16) [c][perm(j)] (strictly-upper blocks stay 0)
-  uint16_t Nh[C * TSTR];      // off-diagonal blocks of N, hi [i][perm(j)] (producers only)
-  uint16_t Nl[C * TSTR];      // off-diagonal blocks of N, lo
+  uint16_t V[C * VSTR];       // V chunk [c][v], single-buffered (written after its last read)
+  uint16_t Nh[NROWS * TSTR];  // N rows 16..63, hi [i - 16][perm(j)] (producers only; row block 0
+  uint16_t Nl[NROWS * TSTR];  // of N is never an operand), lo
   float Nd[4 * 16 * DSTR];    // diagonal 16x16 blocks of N (fp32)
   float gam[2][C];            // gamma_c (inclusive cumsum of the log gates)
   float bet[2][C];            // beta_c
@@ -95,6 +98,19 @@ __device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
 __device__ __forceinline__ int perm32(int r) { return ((r & 15) >> 2) * 8 + ((r >> 4) << 2) + (r & 3); }
 __device__ __forceinline__ int perm(int x) { return (x & ~31) + perm32(x & 31); }
 
+// K/Q tiles: element (r, q) (q = permuted column) lives in 16-byte slot
+// (q / 8) ^ sigma(r) of row r.  sigma swaps bits 1 and 2 of r (and keeps bits 0
+// and 3): eight consecutive rows then hit eight different slots (row-operand
+// reads are conflict-free), and the four rows of a transposed read split over
+// two slot ranges.
+__device__ __forceinline__ int kq_sigma(int r) { return (r & 9) | ((r & 2) << 1) | ((r & 4) >> 1); }
+__device__ __forceinline__ int kq_off(int r, int q) { return r * KSTR + (((q >> 3) ^ kq_sigma(r)) << 3) + (q & 7); }
+
+// Operand row of a K/Q tile: rows row0 + lane%16, contraction block ks.
+__device__ __forceinline__ uint4 frag_kq(const uint16_t* tile, int row0, int ks, int lane) {
+  return *reinterpret_cast<const uint4*>(tile + kq_off(row0 + (lane & 15), 32 * ks + 8 * (lane >> 4)));
+}
+
 // Operand row: rows row0 + lane%16, contraction block ks (32 wide), from a tile
 // stored with permuted columns.
 __device__ __forceinline__ uint4 frag(const uint16_t* tile, int stride, int row0, int ks, int lane) {
@@ -115,10 +131,22 @@ __device__ __forceinline__ uint2 col4_tr(const uint16_t* tile, int stride, int k
   return read_tr(tile + (k0 + 4 * g + (j >> 2)) * stride + perm(col0 + 4 * (j & 3)));
 }
 
-// Operand column: column col0 + lane%16, contraction rows k0 + kappa(g, s).
-__device__ __forceinline__ uint4 frag_tr(const uint16_t* tile, int stride, int k0, int col0, int lane) {
-  const uint2 a = col4_tr(tile, stride, k0, col0, lane);
-  const uint2 b = col4_tr(tile, stride, k0 + 16, col0, lane);
+// The same for a tile with plain column order.
+__device__ __forceinline__ uint2 col4_tr_plain(const uint16_t* tile, int stride, int k0, int col0, int lane) {
+  const int j = lane & 15, g = lane >> 4;
+  return read_tr(tile + (k0 + 4 * g + (j >> 2)) * stride + col0 + 4 * (j & 3));
+}
+
+
+// Operand column of the K tile: column col0 + lane%16 (of the unpermuted k
+// index), contraction rows k0 + kappa(g, s); the K tile form of frag_tr.
+__device__ __forceinline__ uint2 col4_tr_k(const uint16_t* tile, int k0, int col0, int lane) {
+  const int j = lane & 15, g = lane >> 4;
+  return read_tr(tile + kq_off(k0 + 4 * g + (j >> 2), perm(col0 + 4 * (j & 3))));
+}
+__device__ __forceinline__ uint4 frag_tr_k(const uint16_t* tile, int k0, int col0, int lane) {
+  const uint2 a = col4_tr_k(tile, k0, col0, lane);
+  const uint2 b = col4_tr_k(tile, k0 + 16, col0, lane);
   return uint4{a.x, a.y, b.x, b.y};
 }
 
@@ -146,14 +174,37 @@ __device__ __forceinline__ int64_t load_cu(const void* cu, int is64, int i) {
   return is64 ? static_cast<const int64_t*>(cu)[i] : int64_t(static_cast<const int32_t*>(cu)[i]);
 }
 
-// Inclusive prefix sum over the 64 lanes of a wavefront.
-__device__ __forceinline__ float wave_inclusive_scan(float x, int lane) {
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) {
-    const float y = __shfl_up(x, off, 64);
-    if (lane >= off) x += y;
-  }
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ float dpp_or_zero(float x) {
+  return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, ROW_MASK, 0xF, true));
+}
+
+// Inclusive prefix sum over the 64 lanes of a wavefront with DPP: shifts by
+// 1, 2, 4, 8 inside each 16-lane row, then lane 15 of rows 0 / 2 into rows 1 / 3
+// (row_bcast:15) and lane 31 into rows 2 and 3 (row_bcast:31).
+__device__ __forceinline__ float wave_inclusive_scan(float x) {
+  x += dpp_or_zero<0x111, 0xF>(x);
+  x += dpp_or_zero<0x112, 0xF>(x);
+  x += dpp_or_zero<0x114, 0xF>(x);
+  x += dpp_or_zero<0x118, 0xF>(x);
+  x += dpp_or_zero<0x142, 0xA>(x);
+  x += dpp_or_zero<0x143, 0xC>(x);
   return x;
+}
+
+constexpr float kLn2 = 0.6931471805599453f;
+
+// Log-space decay -exp(A_log) * softplus(a + dt_bias) (torch threshold 20) with
+// the hardware exp2/log2; neg_decay = -exp(A_log).  For very negative arguments
+// log(1 + e^x) loses its relative accuracy but stays within ~1e-7 absolutely.
+__device__ __forceinline__ float fast_log_gate(float neg_decay, float x) {
+  const float t = __builtin_amdgcn_exp2f(x * 1.4426950408889634f);
+  const float sp = __builtin_amdgcn_logf(1.f + t) * kLn2;
+  return neg_decay * (x > 20.f ? x : sp);
+}
+
+__device__ __forceinline__ float fast_sigmoid(float x) {
+  return __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-x * 1.4426950408889634f));
 }
 
 // Sum over the four 16-lane rows of a wavefront (lanes j, j+16, j+32, j+48):
@@ -209,39 +260,50 @@ struct TileJob {
   int kind, I, J;
 };
 
+__device__ __forceinline__ f32x4 ld4(const float* p) {
+  const float4 x = *reinterpret_cast<const float4*>(p);
+  return f32x4{x.x, x.y, x.z, x.w};
+}
+
+// Branch-free epilogues: gamma is non-increasing along the chunk, so every
+// exponent kept is <= 0; the masked ones are clamped to 0 before the select.
 __device__ __forceinline__ void tile_epilogue(PrefillSmem& sm, const ChunkBufs& cb, const TileJob t, const f32x4& acc,
-                                              int lane) {
+                                              float scale, int lane) {
   const int g = lane >> 4, n16 = lane & 15;
   if (t.kind == 0) {
     // acc[i] = k_r . k_c, r = 16I + 4g + i, c = 16I + n16
-    const int c = 16 * t.I + n16;
-    const float gc = cb.gam[c];
+    const float gc = cb.gam[16 * t.I + n16];
+    const f32x4 gr = ld4(cb.gam + 16 * t.I + 4 * g), br = ld4(cb.bet + 16 * t.I + 4 * g);
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int ri = 4 * g + i, r = 16 * t.I + ri;
-      sm.Nd[(t.I * 16 + ri) * DSTR + n16] = ri > n16 ? cb.bet[r] * exp_le0(cb.gam[r] - gc) * acc[i] : 0.f;
+      const int ri = 4 * g + i;
+      const float x = br[i] * exp_le0(fminf(gr[i] - gc, 0.f)) * acc[i];
+      sm.Nd[(t.I * 16 + ri) * DSTR + n16] = ri > n16 ? x : 0.f;
     }
   } else if (t.kind == 1) {
-    // acc[i] = k_c . k_r, c = 16J + 4g + i, r = 16I + n16  ->  N[r][c]
+    // acc[i] = k_c . k_r, c = 16J + 4g + i, r = 16I + n16  ->  N[r][c]  (r > c)
     const int r = 16 * t.I + n16;
     const float gr = cb.gam[r], br = cb.bet[r];
+    const f32x4 gcv = ld4(cb.gam + 16 * t.J + 4 * g);
     f32x4 x;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) x[i] = br * exp_le0(gr - cb.gam[16 * t.J + 4 * g + i]) * acc[i];
+    for (int i = 0; i < 4; ++i) x[i] = br * exp_le0(fminf(gr - gcv[i], 0.f)) * acc[i];
     uint2 hi, lo;
     split4(x, hi, lo);
-    const int pos = r * TSTR + perm(16 * t.J + 4 * g);
+    const int pos = (r - 16) * TSTR + perm(16 * t.J + 4 * g);
     *reinterpret_cast<uint2*>(sm.Nh + pos) = hi;
     *reinterpret_cast<uint2*>(sm.Nl + pos) = lo;
   } else {
-    // acc[i] = k_j . q_c, j = 16J + 4g + i, c = 16I + n16  ->  P[c][j]
+    // acc[i] = k_j . q_c, j = 16J + 4g + i, c = 16I + n16  ->  P[c][j]  (j <= c),
+    // with the output scale folded in
     const int c = 16 * t.I + n16;
     const float gc = cb.gam[c];
+    const f32x4 gj = ld4(cb.gam + 16 * t.J + 4 * g);
     float pv[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const int j = 16 * t.J + 4 * g + i;
-      pv[i] = j <= c ? exp_le0(gc - cb.gam[j]) * acc[i] : 0.f;
+      const float x = exp_le0(fminf(gc - gj[i], 0.f)) * (acc[i] * scale);
+      pv[i] = 16 * t.J + 4 * g + i <= c ? x : 0.f;
     }
     *reinterpret_cast<uint2*>(cb.P + c * TSTR + perm(16 * t.J + 4 * g)) =
         uint2{pack_bf16x2(pv[0], pv[1]), pack_bf16x2(pv[2], pv[3])};
@@ -249,44 +311,72 @@ __device__ __forceinline__ void tile_epilogue(PrefillSmem& sm, const ChunkBufs& 
 }
 
 template <int NJ>
-__device__ __forceinline__ void run_tiles(PrefillSmem& sm, const ChunkBufs& cb, const TileJob (&jobs)[NJ], int lane) {
+__device__ __forceinline__ void run_tiles(PrefillSmem& sm, const ChunkBufs& cb, const TileJob (&jobs)[NJ], float scale,
+                                          int lane) {
   f32x4 acc[NJ];
 #pragma unroll
   for (int t = 0; t < NJ; ++t) acc[t] = zero4();
-#pragma unroll 1
-  for (int ks = 0; ks < 4; ++ks) {
+  uint4 a[NJ][4], b[NJ][4];  // all operands first: one round of LDS latency
 #pragma unroll
-    for (int t = 0; t < NJ; ++t) {
-      const TileJob j = jobs[t];
-      const int arow = j.kind == 0 ? 16 * j.I : 16 * j.J;
-      const uint16_t* btile = j.kind == 2 ? cb.Q : cb.K;
-      acc[t] = mfma(frag(cb.K, KSTR, arow, ks, lane), frag(btile, KSTR, 16 * j.I, ks, lane), acc[t]);
+  for (int t = 0; t < NJ; ++t) {
+    const TileJob j = jobs[t];
+    const int arow = j.kind == 0 ? 16 * j.I : 16 * j.J;
+    const uint16_t* btile = j.kind == 2 ? cb.Q : cb.K;
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      a[t][ks] = frag_kq(cb.K, arow, ks, lane);
+      b[t][ks] = frag_kq(btile, 16 * j.I, ks, lane);
     }
   }
 #pragma unroll
-  for (int t = 0; t < NJ; ++t) tile_epilogue(sm, cb, jobs[t], acc[t], lane);
+  for (int ks = 0; ks < 4; ++ks)
+#pragma unroll
+    for (int t = 0; t < NJ; ++t) acc[t] = mfma(a[t][ks], b[t][ks], acc[t]);
+#pragma unroll
+  for (int t = 0; t < NJ; ++t) tile_epilogue(sm, cb, jobs[t], acc[t], scale, lane);
 }
 
-// Diagonal block I of T~: D_I = (I + N_II)^-1 by forward substitution, written
-// to Th/Tl (unit diagonal and zero upper part included).  One wavefront: lane
-// (r, j) = (lane/16, lane%16) follows column j and sums the terms m = 4q + r of
-// each row; the four partial sums are combined across rows.
+// Diagonal block I of T~: D_I = (I + N_II)^-1 by blocked forward substitution,
+// written to Th/Tl (unit diagonal and zero upper part included).  One
+// wavefront: lane (r, j) = (lane/16, lane%16) follows column j, x = D_I[:, j]:
+//   x_i = delta_ij (i <= j),  x_i = -sum_{m < i} N[i][m] x_m (i > j).
+// Rows are taken four at a time (b = 0..3): the terms from earlier row groups
+// are split over the four lanes of a column by m mod 4 and combined across rows;
+// the four rows of a group then follow each other inside the group.
 __device__ __forceinline__ void solve_diagonal_block(const PrefillSmem& sm, const ChunkBufs& cb, int I, int lane) {
   const int r = lane >> 4, j = lane & 15;
   const float* nb = sm.Nd + I * 16 * DSTR;
-  float xr[4];  // xr[q] = x[4q + r], x = column j of D_I
+  // Operands first: cross terms N[i][4q + r] (q < i / 4) and the 4x4 diagonal
+  // sub-blocks N[i][4(i / 4) .. +3].
+  float cross[16][3];
+  f32x4 diag[16];
 #pragma unroll
-  for (int q = 0; q < 4; ++q) xr[q] = (4 * q + r == j) ? 1.f : 0.f;
+  for (int i = 4; i < 16; ++i)
 #pragma unroll
-  for (int i = 1; i < 16; ++i) {
-    // x_i = -sum_{m < i} N[i][m] x_m below the diagonal; N[i][m] = 0 for m >= i
-    // (stored zeros), so whole groups of four terms may be summed.
-    float part = 0.f;
+    for (int q = 0; q < i / 4; ++q) cross[i][q] = nb[i * DSTR + 4 * q + r];
 #pragma unroll
-    for (int q = 0; q < (i + 3) / 4; ++q) part += nb[i * DSTR + 4 * q + r] * xr[q];
-    const float tot = sum_rows(part);
-    const float xi = (i > j) ? -tot : (i == j ? 1.f : 0.f);
-    if (r == (i & 3)) xr[i >> 2] = xi;
+  for (int i = 0; i < 16; ++i) diag[i] = ld4(nb + i * DSTR + 4 * (i / 4));
+  float xr[4];  // xr[q] = x[4q + r]
+#pragma unroll
+  for (int b = 0; b < 4; ++b) {
+    float tot[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      float part = 0.f;
+#pragma unroll
+      for (int q = 0; q < b; ++q) part += cross[4 * b + e][q] * xr[q];
+      tot[e] = b > 0 ? sum_rows(part) : 0.f;
+    }
+    float x[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int i = 4 * b + e;
+      float acc = tot[e];
+#pragma unroll
+      for (int e2 = 0; e2 < e; ++e2) acc += diag[i][e2] * x[e2];
+      x[e] = i > j ? -acc : (i == j ? 1.f : 0.f);
+    }
+    xr[b] = r == 0 ? x[0] : (r == 1 ? x[1] : (r == 2 ? x[2] : x[3]));
   }
   const int col = perm(16 * I + j);
 #pragma unroll
@@ -298,53 +388,48 @@ __device__ __forceinline__ void solve_diagonal_block(const PrefillSmem& sm, cons
   }
 }
 
-// B operand (hi/lo) from an fp32 accumulator tile placed in one half of a
-// 32-wide contraction block, the other half zero.
-__device__ __forceinline__ void acc_to_b(const f32x4& t, bool upper_half, uint4& bh, uint4& bl) {
+// 16x16x16 MFMA (one 16-wide contraction block): lane l supplies A[l%16][4g..4g+3]
+// and B[4g..4g+3][l%16], g = l/16 -- the lower half of the 32-wide convention.
+__device__ __forceinline__ f32x4 mfma16(const uint2& a, const uint2& b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4, a), __builtin_bit_cast(i16x4, b), c, 0,
+                                                   0, 0);
+}
+
+struct Pair2 {  // bf16 hi / lo parts of a 16x16x16 operand
   uint2 h, l;
-  split4(t, h, l);
-  bh = upper_half ? uint4{0u, 0u, h.x, h.y} : uint4{h.x, h.y, 0u, 0u};
-  bl = upper_half ? uint4{0u, 0u, l.x, l.y} : uint4{l.x, l.y, 0u, 0u};
-}
-
-// B operand (hi/lo) of the diagonal block D_J, read from Th/Tl, in its half of
-// contraction block J/2, the other half zero.
-__device__ __forceinline__ void diag_to_b(const ChunkBufs& cb, int J, uint4& bh, uint4& bl, int lane) {
-  const uint2 h = col4_tr(cb.Th, TSTR, 16 * J, 16 * J, lane);
-  const uint2 l = col4_tr(cb.Tl, TSTR, 16 * J, 16 * J, lane);
-  const bool upper = J & 1;
-  bh = upper ? uint4{0u, 0u, h.x, h.y} : uint4{h.x, h.y, 0u, 0u};
-  bl = upper ? uint4{0u, 0u, l.x, l.y} : uint4{l.x, l.y, 0u, 0u};
-}
-
-// Combine two operands that occupy disjoint halves of a contraction block.
-__device__ __forceinline__ uint4 or4(const uint4& a, const uint4& b) {
-  return uint4{a.x | b.x, a.y | b.y, a.z | b.z, a.w | b.w};
-}
-
-// Row block I of a hi/lo tile pair over contraction block q, as A operands.
-struct OpPair {
-  uint4 h, l;
 };
-__device__ __forceinline__ OpPair rows_of(const uint16_t* th, const uint16_t* tl, int I, int q, int lane) {
-  return OpPair{frag(th, TSTR, 16 * I, q, lane), frag(tl, TSTR, 16 * I, q, lane)};
-}
 
-// acc += A * B with A and B given as hi/lo pairs (three passes).
-__device__ __forceinline__ f32x4 mul3(f32x4 acc, const OpPair& a, const uint4& bh, const uint4& bl) {
-  acc = mfma(a.h, bh, acc);
-  acc = mfma(a.h, bl, acc);
-  acc = mfma(a.l, bh, acc);
+// acc += A B, both as hi/lo pairs (three passes).
+__device__ __forceinline__ f32x4 mul3_16(f32x4 acc, const Pair2& a, const Pair2& b) {
+  acc = mfma16(a.h, b.h, acc);
+  acc = mfma16(a.h, b.l, acc);
+  acc = mfma16(a.l, b.h, acc);
   return acc;
 }
 
-// X_IJ = -D_I G; written to Th/Tl and returned.  dI: row block I of T~ over
-// contraction block I/2 with the half that is not D_I masked off.
-__device__ __forceinline__ f32x4 finish_block(const ChunkBufs& cb, const f32x4& G, const OpPair& dI, int I, int J,
+// B operand from an fp32 accumulator tile.
+__device__ __forceinline__ Pair2 acc_b(const f32x4& t) {
+  Pair2 r;
+  split4(t, r.h, r.l);
+  return r;
+}
+
+// A operand of the 16x16 block (I, J) of a hi/lo tile pair with permuted columns
+// (row0 = first row held by the tiles).
+__device__ __forceinline__ Pair2 block_a(const uint16_t* th, const uint16_t* tl, int row0, int I, int J, int lane) {
+  const int off = (16 * I - row0 + (lane & 15)) * TSTR + perm(16 * J + 4 * (lane >> 4));
+  return Pair2{*reinterpret_cast<const uint2*>(th + off), *reinterpret_cast<const uint2*>(tl + off)};
+}
+
+// B operand of the diagonal block D_J of T~.
+__device__ __forceinline__ Pair2 diag_b(const ChunkBufs& cb, int J, int lane) {
+  return Pair2{col4_tr(cb.Th, TSTR, 16 * J, 16 * J, lane), col4_tr(cb.Tl, TSTR, 16 * J, 16 * J, lane)};
+}
+
+// X_IJ = D_I (-G): written to Th/Tl and returned.
+__device__ __forceinline__ f32x4 finish_block(const ChunkBufs& cb, const f32x4& G, const Pair2& dI, int I, int J,
                                               int lane) {
-  uint4 bh, bl;
-  acc_to_b(G, I & 1, bh, bl);
-  const f32x4 X = -mul3(zero4(), dI, bh, bl);
+  const f32x4 X = mul3_16(zero4(), dI, acc_b(-G));
   const int g = lane >> 4, col = perm(16 * J + (lane & 15));
 #pragma unroll
   for (int i = 0; i < 4; ++i) {
@@ -359,47 +444,31 @@ __device__ __forceinline__ f32x4 finish_block(const ChunkBufs& cb, const f32x4& 
 //   X_IJ = -D_I G_IJ,  G_IJ = sum_{K=J}^{I-1} N_IK X_KJ  (X_JJ = D_J)
 // Level 1: (1,0) (2,1) (3,2); level 2: (2,0) (3,1); level 3: (3,0).  Every LDS
 // operand is read before the first block store (the stores would otherwise
-// order the later reads behind them); the X blocks of earlier levels stay in
-// registers.
+// order the later reads behind them), the products that involve only diagonal
+// blocks are formed ahead of the chain, and the X blocks of earlier levels stay
+// in registers.
 __device__ __forceinline__ void solve_offdiagonal(const PrefillSmem& sm, const ChunkBufs& cb, int lane) {
-  uint4 d0h, d0l, d1h, d1l, d2h, d2l;
-  diag_to_b(cb, 0, d0h, d0l, lane);
-  diag_to_b(cb, 1, d1h, d1l, lane);
-  diag_to_b(cb, 2, d2h, d2l, lane);
-  // Row blocks of N: (1 | q0) = [N10 0], (2 | q0) = [N20 N21], (3 | q0) = [N30 N31], (3 | q1) = [N32 0].
-  const OpPair n1 = rows_of(sm.Nh, sm.Nl, 1, 0, lane);
-  const OpPair n2 = rows_of(sm.Nh, sm.Nl, 2, 0, lane);
-  const OpPair n30 = rows_of(sm.Nh, sm.Nl, 3, 0, lane);
-  const OpPair n31 = rows_of(sm.Nh, sm.Nl, 3, 1, lane);
-  // D_I as A operands; the other half of the contraction block may hold an
-  // earlier chunk's off-diagonal block and is masked off.
-  OpPair a1 = rows_of(cb.Th, cb.Tl, 1, 0, lane);
-  OpPair a2 = rows_of(cb.Th, cb.Tl, 2, 1, lane);
-  OpPair a3 = rows_of(cb.Th, cb.Tl, 3, 1, lane);
-  a1.h.x = a1.h.y = a1.l.x = a1.l.y = 0u;
-  a2.h.z = a2.h.w = a2.l.z = a2.l.w = 0u;
-  a3.h.x = a3.h.y = a3.l.x = a3.l.y = 0u;
+  const Pair2 d0 = diag_b(cb, 0, lane), d1 = diag_b(cb, 1, lane), d2 = diag_b(cb, 2, lane);
+  const Pair2 a1 = block_a(cb.Th, cb.Tl, 0, 1, 1, lane), a2 = block_a(cb.Th, cb.Tl, 0, 2, 2, lane),
+              a3 = block_a(cb.Th, cb.Tl, 0, 3, 3, lane);
+  const Pair2 n10 = block_a(sm.Nh, sm.Nl, 16, 1, 0, lane), n20 = block_a(sm.Nh, sm.Nl, 16, 2, 0, lane),
+              n21 = block_a(sm.Nh, sm.Nl, 16, 2, 1, lane), n30 = block_a(sm.Nh, sm.Nl, 16, 3, 0, lane),
+              n31 = block_a(sm.Nh, sm.Nl, 16, 3, 1, lane), n32 = block_a(sm.Nh, sm.Nl, 16, 3, 2, lane);
+  // products of diagonal blocks only
+  const f32x4 p20 = mul3_16(zero4(), n20, d0);
+  const f32x4 p31 = mul3_16(zero4(), n31, d1);
+  const f32x4 p30 = mul3_16(zero4(), n30, d0);
   // level 1
-  const f32x4 g10 = mul3(zero4(), n1, d0h, d0l);
-  const f32x4 g21 = mul3(zero4(), n2, d1h, d1l);
-  const f32x4 g32 = mul3(zero4(), n31, d2h, d2l);
-  const f32x4 x10 = finish_block(cb, g10, a1, 1, 0, lane);
-  const f32x4 x21 = finish_block(cb, g21, a2, 2, 1, lane);
-  finish_block(cb, g32, a3, 3, 2, lane);
+  const f32x4 x10 = finish_block(cb, mul3_16(zero4(), n10, d0), a1, 1, 0, lane);
+  const f32x4 x21 = finish_block(cb, mul3_16(zero4(), n21, d1), a2, 2, 1, lane);
+  finish_block(cb, mul3_16(zero4(), n32, d2), a3, 3, 2, lane);
   // level 2
-  uint4 x10h, x10l, x21h, x21l;
-  acc_to_b(x10, true, x10h, x10l);   // row block 1: upper half of contraction block 0
-  acc_to_b(x21, false, x21h, x21l);  // row block 2: lower half of contraction block 1
-  const uint4 c0h = or4(d0h, x10h), c0l = or4(d0l, x10l);  // column block 0, rows 0-31
-  const f32x4 g20 = mul3(zero4(), n2, c0h, c0l);
-  const f32x4 g31 = mul3(mul3(zero4(), n30, d1h, d1l), n31, x21h, x21l);
-  const f32x4 x20 = finish_block(cb, g20, a2, 2, 0, lane);
-  finish_block(cb, g31, a3, 3, 1, lane);
+  const Pair2 b10 = acc_b(x10), b21 = acc_b(x21);
+  const f32x4 x20 = finish_block(cb, mul3_16(p20, n21, b10), a2, 2, 0, lane);
+  finish_block(cb, mul3_16(p31, n32, b21), a3, 3, 1, lane);
+  const f32x4 g30 = mul3_16(p30, n31, b10);
   // level 3
-  uint4 x20h, x20l;
-  acc_to_b(x20, false, x20h, x20l);
-  const f32x4 g30 = mul3(mul3(zero4(), n30, c0h, c0l), n31, x20h, x20l);
-  finish_block(cb, g30, a3, 3, 0, lane);
+  finish_block(cb, mul3_16(g30, n32, acc_b(x20)), a3, 3, 0, lane);
 }
 
 struct ProducerPrefetch {
@@ -432,9 +501,10 @@ __device__ __forceinline__ void producer_prefetch(const PrefillArgs& p, int64_t 
 __device__ __forceinline__ void producer_loop(PrefillSmem& sm, const PrefillArgs& p, int64_t s0, int64_t s1,
                                               int nchunks, int h, int hq, int hk, int pw, int lane0) {
   const int pt = pw * 64 + lane0;
-  const float A_log = p.A_log[h];
+  const float neg_decay = -expf(p.A_log[h]);
   const float dt_bias = p.dt_bias[h];
   ProducerPrefetch f;
+  uint4 fv[4];
   producer_prefetch(p, s0, int(s1 - s0 < C ? s1 - s0 : C), h, hq, hk, pt, f);
   lds_barrier();  // LDS clearing done (matched by the consumers)
 
@@ -454,46 +524,57 @@ __device__ __forceinline__ void producer_loop(PrefillSmem& sm, const PrefillArgs
       for (int it = 0; it < 4; ++it) {
         const int seg = pt + it * NPROD, c = seg >> 4, sg = seg & 15;
         const int col0 = (8 * sg) & ~31, r0 = (8 * sg) & 31;
-        const int pa = c * KSTR + col0 + perm32(r0), pb = c * KSTR + col0 + perm32(r0 + 4);
+        const int pa = kq_off(c, col0 + perm32(r0)), pb = kq_off(c, col0 + perm32(r0 + 4));
         *reinterpret_cast<uint2*>(cb.K + pa) = uint2{f.k[it].x, f.k[it].y};
         *reinterpret_cast<uint2*>(cb.K + pb) = uint2{f.k[it].z, f.k[it].w};
         *reinterpret_cast<uint2*>(cb.Q + pa) = uint2{f.q[it].x, f.q[it].y};
         *reinterpret_cast<uint2*>(cb.Q + pb) = uint2{f.q[it].z, f.q[it].w};
       }
       if (pw == 0) {
-        const float lg = lane < clen ? log_gate(A_log, bf16_to_f32(f.a), dt_bias) : 0.f;
-        const float bt = lane < clen ? sigmoidf_(bf16_to_f32(f.b)) : 0.f;
-        const float gm = wave_inclusive_scan(lg, lane);
+        const float lg = lane < clen ? fast_log_gate(neg_decay, bf16_to_f32(f.a) + dt_bias) : 0.f;
+        const float bt = lane < clen ? fast_sigmoid(bf16_to_f32(f.b)) : 0.f;
+        const float gm = wave_inclusive_scan(lg);
         const float glast = readlane_f(gm, clen - 1);
         cb.gam[lane] = gm;
         cb.bet[lane] = bt;
-        cb.eg[lane] = expf(gm);
-        cb.dd[lane] = expf(glast - gm);
+        cb.eg[lane] = exp_le0(gm);
+        cb.dd[lane] = exp_le0(glast - gm);
+      }
+      // V of this chunk into registers; staged at the end of the tick, after the
+      // consumers' last read of the previous chunk's V.
+#pragma unroll
+      for (int it = 0; it < 4; ++it) {
+        const int seg = pt + it * NPROD, c = seg >> 4, sg = seg & 15;
+        fv[it] = uint4{0u, 0u, 0u, 0u};
+        if (c < clen) fv[it] = *reinterpret_cast<const uint4*>(p.v + ((cs + c) * p.Hv + h) * D + 8 * sg);
       }
     }
     lds_barrier();
+    // Sub-phases 2 and 3 of the producers are the longer ones: their waves go
+    // ahead of the consumer wave sharing the SIMD.
+    __builtin_amdgcn_s_setprio(1);
 
     // 2: N tiles (and two P tiles), diagonal blocks of T~
     if (work) {
       switch (pw) {
         case 0: {
           const TileJob jobs[3] = {{0, 0, 0}, {1, 1, 0}, {1, 2, 0}};
-          run_tiles(sm, cb, jobs, lane);
+          run_tiles(sm, cb, jobs, p.scale, lane);
           break;
         }
         case 1: {
           const TileJob jobs[3] = {{0, 1, 1}, {1, 3, 0}, {1, 2, 1}};
-          run_tiles(sm, cb, jobs, lane);
+          run_tiles(sm, cb, jobs, p.scale, lane);
           break;
         }
         case 2: {
           const TileJob jobs[3] = {{0, 2, 2}, {1, 3, 1}, {1, 3, 2}};
-          run_tiles(sm, cb, jobs, lane);
+          run_tiles(sm, cb, jobs, p.scale, lane);
           break;
         }
         default: {
           const TileJob jobs[3] = {{0, 3, 3}, {2, 3, 3}, {2, 3, 2}};
-          run_tiles(sm, cb, jobs, lane);
+          run_tiles(sm, cb, jobs, p.scale, lane);
           break;
         }
       }
@@ -508,26 +589,32 @@ __device__ __forceinline__ void producer_loop(PrefillSmem& sm, const PrefillArgs
       switch (pw) {
         case 0: {
           const TileJob jobs[3] = {{2, 0, 0}, {2, 1, 0}, {2, 1, 1}};
-          run_tiles(sm, cb, jobs, lane);
+          run_tiles(sm, cb, jobs, p.scale, lane);
           break;
         }
         case 1: {
           const TileJob jobs[3] = {{2, 2, 0}, {2, 2, 1}, {2, 2, 2}};
-          run_tiles(sm, cb, jobs, lane);
+          run_tiles(sm, cb, jobs, p.scale, lane);
           break;
         }
         case 2: {
           const TileJob jobs[2] = {{2, 3, 0}, {2, 3, 1}};
-          run_tiles(sm, cb, jobs, lane);
+          run_tiles(sm, cb, jobs, p.scale, lane);
           break;
         }
         default:
           solve_offdiagonal(sm, cb, lane);
           break;
       }
+#pragma unroll
+      for (int it = 0; it < 4; ++it) {
+        const int seg = pt + it * NPROD;
+        *reinterpret_cast<uint4*>(sm.V + (seg >> 4) * VSTR + 8 * (seg & 15)) = fv[it];
+      }
       const int64_t ncs = cs + C;
       if (ncs < s1) producer_prefetch(p, ncs, int(s1 - ncs < C ? s1 - ncs : C), h, hq, hk, pt, f);
     }
+    __builtin_amdgcn_s_setprio(0);
     lds_barrier();
   }
 }
@@ -551,8 +638,8 @@ __device__ __forceinline__ void retrieve(const ChunkBufs& cb, const f32x4 (&S)[2
     for (int vt = 0; vt < 2; ++vt) split_pack(S[vt][2 * ks], S[vt][2 * ks + 1], Sh[vt], Sl[vt]);
 #pragma unroll
     for (int ct = 0; ct < 4; ++ct) {
-      const uint4 ak = frag(cb.K, KSTR, 16 * ct, ks, lane);
-      const uint4 bq = frag(cb.Q, KSTR, 16 * ct, ks, lane);
+      const uint4 ak = frag_kq(cb.K, 16 * ct, ks, lane);
+      const uint4 bq = frag_kq(cb.Q, 16 * ct, ks, lane);
 #pragma unroll
       for (int vt = 0; vt < 2; ++vt) {
         Xk[ct][vt] = mfma(ak, Sh[vt], Xk[ct][vt]);
@@ -562,35 +649,6 @@ __device__ __forceinline__ void retrieve(const ChunkBufs& cb, const f32x4 (&S)[2
     }
     __builtin_amdgcn_sched_barrier(0);  // bound the number of operand loads in flight
   }
-}
-
-// V[c][v] for c = 16ct + 4g + i, v = 32w + 16vt + n16 of the chunk at cs, as raw
-// bf16 bits.  Rows past the chunk end load the last row (in bounds) and are
-// masked when used, so the loads need no branches and can stay in flight.
-__device__ __forceinline__ void load_v(const PrefillArgs& p, int64_t cs, int clen, int h, int wave, int lane,
-                                       uint16_t (&vr)[4][2][4]) {
-  const int64_t vstride = int64_t(p.Hv) * D;
-  const uint16_t* base = p.v + cs * vstride + int64_t(h) * D + 32 * wave + (lane & 15);
-  const int g = lane >> 4;
-#pragma unroll
-  for (int ct = 0; ct < 4; ++ct)
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int c = 16 * ct + 4 * g + i;
-      const int64_t row = c < clen ? c : clen - 1;
-#pragma unroll
-      for (int vt = 0; vt < 2; ++vt) vr[ct][vt][i] = base[row * vstride + 16 * vt];
-    }
-}
-
-__device__ __forceinline__ void pack_v(const uint16_t (&vr)[4][2][4], uint32_t (&vbits)[4][2][2]) {
-#pragma unroll
-  for (int ct = 0; ct < 4; ++ct)
-#pragma unroll
-    for (int vt = 0; vt < 2; ++vt) {
-      vbits[ct][vt][0] = uint32_t(vr[ct][vt][0]) | (uint32_t(vr[ct][vt][1]) << 16);
-      vbits[ct][vt][1] = uint32_t(vr[ct][vt][2]) | (uint32_t(vr[ct][vt][3]) << 16);
-    }
 }
 
 // The consumer loop: tick t (>= 1) advances the state through chunk t-1 from the
@@ -603,11 +661,9 @@ __device__ __forceinline__ void consumer_loop(PrefillSmem& sm, const PrefillArgs
   lds_barrier();
   lds_barrier();
   const int64_t vstride = int64_t(p.Hv) * D;
-  // V of the chunk processed next, loaded a tick ahead and packed in pairs of rows.
-  uint16_t vr[4][2][4];
-  uint32_t vbits[4][2][2];
-  load_v(p, s0, int(s1 - s0 < C ? s1 - s0 : C), h, wave, lane0, vr);
-  pack_v(vr, vbits);
+  int orow[4];  // element offset of output row 16ct + lane%16 from the chunk start
+#pragma unroll
+  for (int ct = 0; ct < 4; ++ct) orow[ct] = (16 * ct + (lane0 & 15)) * int(vstride);
   for (int t = 1; t <= nchunks; ++t) {
     int lane = lane0;
     asm volatile("" : "+v"(lane));
@@ -629,14 +685,14 @@ __device__ __forceinline__ void consumer_loop(PrefillSmem& sm, const PrefillArgs
       const float4 ec = *reinterpret_cast<const float4*>(cb.eg + 16 * ct + 4 * g);
       const float b4[4] = {bc.x, bc.y, bc.z, bc.w}, e4[4] = {ec.x, ec.y, ec.z, ec.w};
 #pragma unroll
-      for (int vt = 0; vt < 2; ++vt)
+      for (int vt = 0; vt < 2; ++vt) {
+        // V rows 16ct + 4g .. +3 of column 32w + 16vt + n16 (zero past the chunk end)
+        const uint2 vv = col4_tr_plain(sm.V, VSTR, 16 * ct, 32 * wave + 16 * vt, lane);
+        const float vf[4] = {bf16lo_f32(vv.x), bf16hi_f32(vv.x), bf16lo_f32(vv.y), bf16hi_f32(vv.y)};
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          const uint32_t w = vbits[ct][vt][i >> 1];
-          const float vf = 16 * ct + 4 * g + i < clen ? ((i & 1) ? bf16hi_f32(w) : bf16lo_f32(w)) : 0.f;
-          Xk[ct][vt][i] = b4[i] * (vf - e4[i] * Xk[ct][vt][i]);
-        }
-      const float ecn = cb.eg[16 * ct + n16];  // e^gamma of output column c = 16ct + n16
+        for (int i = 0; i < 4; ++i) Xk[ct][vt][i] = b4[i] * (vf[i] - e4[i] * Xk[ct][vt][i]);
+      }
+      const float ecn = cb.eg[16 * ct + n16] * p.scale;  // scale e^gamma of output column c = 16ct + n16
 #pragma unroll
       for (int vt = 0; vt < 2; ++vt) Xq[vt][ct] = Xq[vt][ct] * ecn;
     }
@@ -663,7 +719,7 @@ __device__ __forceinline__ void consumer_loop(PrefillSmem& sm, const PrefillArgs
         }
       }
     }
-    // o^T = e^gamma (S Q^T) + v_new^T P^T (rows v, cols c); P is lower triangular.
+    // o^T = scale e^gamma (S Q^T) + v_new^T (scale P)^T (rows v, cols c); P is lower triangular.
 #pragma unroll
     for (int js = 0; js < 2; ++js) {
       uint4 vb[2];
@@ -677,25 +733,20 @@ __device__ __forceinline__ void consumer_loop(PrefillSmem& sm, const PrefillArgs
       }
     }
     // Lane holds o[c = 16ct + n16][v = 32w + 16vt + 4g .. +3]: one 8-byte store each.
+    uint16_t* obase = p.out + cs * vstride + (int64_t(h) * D + 32 * wave + 4 * g);
 #pragma unroll
     for (int ct = 0; ct < 4; ++ct) {
-      const int c = 16 * ct + n16;
-      if (c < clen) {
+      if (16 * ct + n16 < clen) {
 #pragma unroll
         for (int vt = 0; vt < 2; ++vt) {
-          const f32x4 o = Xq[vt][ct] * p.scale;
-          *reinterpret_cast<uint2*>(p.out + (cs + c) * vstride + int64_t(h) * D + 32 * wave + 16 * vt + 4 * g) =
-              uint2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
+          const f32x4& o = Xq[vt][ct];
+          *reinterpret_cast<uint2*>(obase + orow[ct] + 16 * vt) = uint2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
         }
       }
     }
     lds_barrier();
 
     // 3: S = e^{gamma_last} S + sum_c K[c]^T (d_c v_new[c]),  d_c = e^{gamma_last - gamma_c}
-    if (t < nchunks) {
-      const int64_t ncs = cs + C;
-      load_v(p, ncs, int(s1 - ncs < C ? s1 - ncs : C), h, wave, lane, vr);
-    }
     const float dlast = cb.eg[clen - 1];
     uint4 Uh[2][2], Ul[2][2];
 #pragma unroll
@@ -712,7 +763,7 @@ __device__ __forceinline__ void consumer_loop(PrefillSmem& sm, const PrefillArgs
       for (int vt = 0; vt < 2; ++vt) S[vt][kt] = S[vt][kt] * dlast;
 #pragma unroll
       for (int js = 0; js < 2; ++js) {
-        const uint4 ak = frag_tr(cb.K, KSTR, 32 * js, 16 * kt, lane);
+        const uint4 ak = frag_tr_k(cb.K, 32 * js, 16 * kt, lane);
 #pragma unroll
         for (int vt = 0; vt < 2; ++vt) {
           S[vt][kt] = mfma(ak, Uh[vt][js], S[vt][kt]);
@@ -720,7 +771,6 @@ __device__ __forceinline__ void consumer_loop(PrefillSmem& sm, const PrefillArgs
         }
       }
     }
-    if (t < nchunks) pack_v(vr, vbits);
     lds_barrier();
   }
 }
@@ -780,8 +830,10 @@ __global__ __launch_bounds__(NTHREADS) void gdn_prefill_kernel(PrefillArgs p) {
       reinterpret_cast<uint4*>(sm.Th[1])[e] = z;
       reinterpret_cast<uint4*>(sm.Tl[0])[e] = z;
       reinterpret_cast<uint4*>(sm.Tl[1])[e] = z;
-      reinterpret_cast<uint4*>(sm.Nh)[e] = z;
-      reinterpret_cast<uint4*>(sm.Nl)[e] = z;
+      if (e < NROWS * TSTR / 8) {
+        reinterpret_cast<uint4*>(sm.Nh)[e] = z;
+        reinterpret_cast<uint4*>(sm.Nl)[e] = z;
+      }
     }
   }
 
