@@ -379,12 +379,14 @@ __device__ __forceinline__ void solve_diagonal_block(const PrefillSmem& sm, cons
     xr[b] = r == 0 ? x[0] : (r == 1 ? x[1] : (r == 2 ? x[2] : x[3]));
   }
   const int col = perm(16 * I + j);
+  uint2 hi, lo;
+  split4(f32x4{xr[0], xr[1], xr[2], xr[3]}, hi, lo);
+  const uint32_t h4[4] = {hi.x, hi.x >> 16, hi.y, hi.y >> 16}, l4[4] = {lo.x, lo.x >> 16, lo.y, lo.y >> 16};
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const int row = 16 * I + 4 * q + r;
-    const uint16_t hi = f32_to_bf16(xr[q]);
-    cb.Th[row * TSTR + col] = hi;
-    cb.Tl[row * TSTR + col] = f32_to_bf16(xr[q] - bf16_to_f32(hi));
+    cb.Th[row * TSTR + col] = uint16_t(h4[q]);
+    cb.Tl[row * TSTR + col] = uint16_t(l4[q]);
   }
 }
 
@@ -426,27 +428,35 @@ __device__ __forceinline__ Pair2 diag_b(const ChunkBufs& cb, int J, int lane) {
   return Pair2{col4_tr(cb.Th, TSTR, 16 * J, 16 * J, lane), col4_tr(cb.Tl, TSTR, 16 * J, 16 * J, lane)};
 }
 
+// Writes an off-diagonal block X_IJ (accumulator layout) to Th/Tl.
+__device__ __forceinline__ void store_block(const ChunkBufs& cb, const f32x4& X, int I, int J, int lane) {
+  const int g = lane >> 4, col = perm(16 * J + (lane & 15));
+  uint2 hi, lo;
+  split4(X, hi, lo);
+  const uint32_t h4[4] = {hi.x, hi.x >> 16, hi.y, hi.y >> 16}, l4[4] = {lo.x, lo.x >> 16, lo.y, lo.y >> 16};
+#pragma unroll
+  for (int i = 0; i < 4; ++i) {
+    cb.Th[(16 * I + 4 * g + i) * TSTR + col] = uint16_t(h4[i]);
+    cb.Tl[(16 * I + 4 * g + i) * TSTR + col] = uint16_t(l4[i]);
+  }
+}
+
 // X_IJ = D_I (-G): written to Th/Tl and returned.
 __device__ __forceinline__ f32x4 finish_block(const ChunkBufs& cb, const f32x4& G, const Pair2& dI, int I, int J,
                                               int lane) {
   const f32x4 X = mul3_16(zero4(), dI, acc_b(-G));
-  const int g = lane >> 4, col = perm(16 * J + (lane & 15));
-#pragma unroll
-  for (int i = 0; i < 4; ++i) {
-    const uint16_t hi = f32_to_bf16(X[i]);
-    cb.Th[(16 * I + 4 * g + i) * TSTR + col] = hi;
-    cb.Tl[(16 * I + 4 * g + i) * TSTR + col] = f32_to_bf16(X[i] - bf16_to_f32(hi));
-  }
+  store_block(cb, X, I, J, lane);
   return X;
 }
 
-// Off-diagonal blocks of T~ (one wavefront):
-//   X_IJ = -D_I G_IJ,  G_IJ = sum_{K=J}^{I-1} N_IK X_KJ  (X_JJ = D_J)
-// Level 1: (1,0) (2,1) (3,2); level 2: (2,0) (3,1); level 3: (3,0).  Every LDS
-// operand is read before the first block store (the stores would otherwise
-// order the later reads behind them), the products that involve only diagonal
-// blocks are formed ahead of the chain, and the X blocks of earlier levels stay
-// in registers.
+// Off-diagonal blocks of T~ (one wavefront), as a 2x2 block inverse over the
+// 32x32 halves:  T~ = [[A^-1, 0], [-B^-1 C A^-1, B^-1]] with
+//   A^-1 = [[D0, 0], [X10, D1]],  B^-1 = [[D2, 0], [X32, D3]],  C = [[N20, N21], [N30, N31]],
+//   X10 = -D1 N10 D0,  X32 = -D3 N32 D2,  M = C A^-1,  [[X20, X21], [X30, X31]] = -B^-1 M.
+// The dependent chain is four products deep (N10 D0 -> X10 -> M20 / M30 -> X20 / X30).
+// X32 is also formed transposed (X32^T = G32^T (-D3)^T) so that its accumulator
+// serves as the A operand of X32 M.  Every LDS operand is read before the first
+// block store.
 __device__ __forceinline__ void solve_offdiagonal(const PrefillSmem& sm, const ChunkBufs& cb, int lane) {
   const Pair2 d0 = diag_b(cb, 0, lane), d1 = diag_b(cb, 1, lane), d2 = diag_b(cb, 2, lane);
   const Pair2 a1 = block_a(cb.Th, cb.Tl, 0, 1, 1, lane), a2 = block_a(cb.Th, cb.Tl, 0, 2, 2, lane),
@@ -455,20 +465,26 @@ __device__ __forceinline__ void solve_offdiagonal(const PrefillSmem& sm, const C
               n21 = block_a(sm.Nh, sm.Nl, 16, 2, 1, lane), n30 = block_a(sm.Nh, sm.Nl, 16, 3, 0, lane),
               n31 = block_a(sm.Nh, sm.Nl, 16, 3, 1, lane), n32 = block_a(sm.Nh, sm.Nl, 16, 3, 2, lane);
   // products of diagonal blocks only
+  const f32x4 g10 = mul3_16(zero4(), n10, d0);
+  const f32x4 g32 = mul3_16(zero4(), n32, d2);
   const f32x4 p20 = mul3_16(zero4(), n20, d0);
-  const f32x4 p31 = mul3_16(zero4(), n31, d1);
   const f32x4 p30 = mul3_16(zero4(), n30, d0);
-  // level 1
-  const f32x4 x10 = finish_block(cb, mul3_16(zero4(), n10, d0), a1, 1, 0, lane);
-  const f32x4 x21 = finish_block(cb, mul3_16(zero4(), n21, d1), a2, 2, 1, lane);
-  finish_block(cb, mul3_16(zero4(), n32, d2), a3, 3, 2, lane);
-  // level 2
-  const Pair2 b10 = acc_b(x10), b21 = acc_b(x21);
-  const f32x4 x20 = finish_block(cb, mul3_16(p20, n21, b10), a2, 2, 0, lane);
-  finish_block(cb, mul3_16(p31, n32, b21), a3, 3, 1, lane);
-  const f32x4 g30 = mul3_16(p30, n31, b10);
-  // level 3
-  finish_block(cb, mul3_16(g30, n32, acc_b(x20)), a3, 3, 0, lane);
+  const f32x4 m21 = mul3_16(zero4(), n21, d1);
+  const f32x4 m31 = mul3_16(zero4(), n31, d1);
+  // X10, X32 (and X32^T)
+  const f32x4 x10 = finish_block(cb, g10, a1, 1, 0, lane);
+  finish_block(cb, g32, a3, 3, 2, lane);
+  const Pair2 x32t = acc_b(mul3_16(zero4(), acc_b(-g32), a3));  // A operand holding X32
+  // M = C A^-1 (column 0 needs X10; column 1 is N21 D1, N31 D1)
+  const Pair2 b10 = acc_b(x10);
+  const Pair2 nm20 = acc_b(-mul3_16(p20, n21, b10));
+  const Pair2 nm30 = acc_b(-mul3_16(p30, n31, b10));
+  const Pair2 nm21 = acc_b(-m21), nm31 = acc_b(-m31);
+  // -B^-1 M
+  store_block(cb, mul3_16(zero4(), a2, nm20), 2, 0, lane);
+  store_block(cb, mul3_16(zero4(), a2, nm21), 2, 1, lane);
+  store_block(cb, mul3_16(mul3_16(zero4(), x32t, nm20), a3, nm30), 3, 0, lane);
+  store_block(cb, mul3_16(mul3_16(zero4(), x32t, nm21), a3, nm31), 3, 1, lane);
 }
 
 struct ProducerPrefetch {
@@ -647,7 +663,6 @@ __device__ __forceinline__ void retrieve(const ChunkBufs& cb, const f32x4 (&S)[2
         Xq[vt][ct] = mfma(Sh[vt], bq, Xq[vt][ct]);
       }
     }
-    __builtin_amdgcn_sched_barrier(0);  // bound the number of operand loads in flight
   }
 }
 
