@@ -59,7 +59,7 @@ constexpr int D = kHeadDim;  // 128
 constexpr int KSTR = 128;    // bf16 row stride of the K and Q tiles (16-byte slots XOR-swizzled by row)
 constexpr int VSTR = 144;    // bf16 row stride of the V tile (rows 32 bytes apart modulo 128)
 constexpr int TSTR = 72;     // bf16 row stride of 64-wide tiles (T~, P, N)
-constexpr int DSTR = 20;     // fp32 row stride of the diagonal N blocks (16-byte aligned rows)
+constexpr int NDB = 16 * 16 + 4;  // floats per diagonal N block (column-major; padded by 16 bytes)
 constexpr int NTHREADS = 512;
 constexpr int NPROD = 256;   // producer threads (waves 4-7)
 constexpr int NROWS = C - 16;  // rows of N kept for the off-diagonal solve
@@ -74,7 +74,7 @@ struct __align__(16) PrefillSmem {
   uint16_t V[C * VSTR];       // V chunk [c][v], single-buffered (written after its last read)
   uint16_t Nh[NROWS * TSTR];  // N rows 16..63, hi [i - 16][perm(j)] (producers only; row block 0
   uint16_t Nl[NROWS * TSTR];  // of N is never an operand), lo
-  float Nd[4 * 16 * DSTR];    // diagonal 16x16 blocks of N (fp32)
+  float Nd[4 * NDB];          // diagonal 16x16 blocks of N (fp32, column-major: [block][col][row])
   float gam[2][C];            // gamma_c (inclusive cumsum of the log gates)
   float bet[2][C];            // beta_c
   float eg[2][C];             // e^{gamma_c}
@@ -252,7 +252,6 @@ __device__ __forceinline__ ChunkBufs chunk_bufs(PrefillSmem& sm, int b) {
 // ---------------------------------------------------------------------------
 
 // Tiles of N and P from the staged K and Q (16x16 tiles, 4 MFMAs each).
-//   kind 0: diagonal block I of N (fp32, into Nd), from tile K_I K_I^T
 //   kind 1: off-diagonal block (I, J), I > J, of N (bf16 hi/lo), from tile
 //           K_J K_I^T so that a lane holds 4 consecutive columns of one row
 //   kind 2: block (I, J), J <= I, of P, from tile K_J Q_I^T
@@ -270,17 +269,7 @@ __device__ __forceinline__ f32x4 ld4(const float* p) {
 __device__ __forceinline__ void tile_epilogue(PrefillSmem& sm, const ChunkBufs& cb, const TileJob t, const f32x4& acc,
                                               float scale, int lane) {
   const int g = lane >> 4, n16 = lane & 15;
-  if (t.kind == 0) {
-    // acc[i] = k_r . k_c, r = 16I + 4g + i, c = 16I + n16
-    const float gc = cb.gam[16 * t.I + n16];
-    const f32x4 gr = ld4(cb.gam + 16 * t.I + 4 * g), br = ld4(cb.bet + 16 * t.I + 4 * g);
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int ri = 4 * g + i;
-      const float x = br[i] * exp_le0(fminf(gr[i] - gc, 0.f)) * acc[i];
-      sm.Nd[(t.I * 16 + ri) * DSTR + n16] = ri > n16 ? x : 0.f;
-    }
-  } else if (t.kind == 1) {
+  if (t.kind == 1) {
     // acc[i] = k_c . k_r, c = 16J + 4g + i, r = 16I + n16  ->  N[r][c]  (r > c)
     const int r = 16 * t.I + n16;
     const float gr = cb.gam[r], br = cb.bet[r];
@@ -320,7 +309,7 @@ __device__ __forceinline__ void run_tiles(PrefillSmem& sm, const ChunkBufs& cb, 
 #pragma unroll
   for (int t = 0; t < NJ; ++t) {
     const TileJob j = jobs[t];
-    const int arow = j.kind == 0 ? 16 * j.I : 16 * j.J;
+    const int arow = 16 * j.J;
     const uint16_t* btile = j.kind == 2 ? cb.Q : cb.K;
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
@@ -336,57 +325,77 @@ __device__ __forceinline__ void run_tiles(PrefillSmem& sm, const ChunkBufs& cb, 
   for (int t = 0; t < NJ; ++t) tile_epilogue(sm, cb, jobs[t], acc[t], scale, lane);
 }
 
-// Diagonal block I of T~: D_I = (I + N_II)^-1 by blocked forward substitution,
-// written to Th/Tl (unit diagonal and zero upper part included).  One
-// wavefront: lane (r, j) = (lane/16, lane%16) follows column j, x = D_I[:, j]:
-//   x_i = delta_ij (i <= j),  x_i = -sum_{m < i} N[i][m] x_m (i > j).
-// Rows are taken four at a time (b = 0..3): the terms from earlier row groups
-// are split over the four lanes of a column by m mod 4 and combined across rows;
-// the four rows of a group then follow each other inside the group.
-__device__ __forceinline__ void solve_diagonal_block(const PrefillSmem& sm, const ChunkBufs& cb, int I, int lane) {
-  const int r = lane >> 4, j = lane & 15;
-  const float* nb = sm.Nd + I * 16 * DSTR;
-  // Operands first: cross terms N[i][4q + r] (q < i / 4) and the 4x4 diagonal
-  // sub-blocks N[i][4(i / 4) .. +3].
-  float cross[16][3];
-  f32x4 diag[16];
+// The four diagonal blocks of T~, D_I = (I + N_II)^-1, on one wavefront.
+// The tiles K_I K_I^T give N_II (scaled as in the off-diagonal epilogue), stored
+// column-major; then lane (r, j) = (lane/16, lane%16) inverts block r, column j,
+// x = D_r[:, j], by right-looking forward substitution:
+//   x_m = delta_mj - a_m,  a_i += N[i][m] x_m  for i > m
+// (for m < j every term is zero, so x_m = 0 there).  The column of N needed at
+// step m is one broadcast read per four rows; no cross-lane traffic.
+__device__ __forceinline__ void diag_blocks(PrefillSmem& sm, const ChunkBufs& cb, int lane) {
+  const int g = lane >> 4, n16 = lane & 15;
+  {
+    uint4 kf[4][4];
 #pragma unroll
-  for (int i = 4; i < 16; ++i)
+    for (int I = 0; I < 4; ++I)
 #pragma unroll
-    for (int q = 0; q < i / 4; ++q) cross[i][q] = nb[i * DSTR + 4 * q + r];
+      for (int ks = 0; ks < 4; ++ks) kf[I][ks] = frag_kq(cb.K, 16 * I, ks, lane);
+    f32x4 acc[4];
 #pragma unroll
-  for (int i = 0; i < 16; ++i) diag[i] = ld4(nb + i * DSTR + 4 * (i / 4));
-  float xr[4];  // xr[q] = x[4q + r]
+    for (int I = 0; I < 4; ++I) acc[I] = zero4();
 #pragma unroll
-  for (int b = 0; b < 4; ++b) {
-    float tot[4];
+    for (int ks = 0; ks < 4; ++ks)
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      float part = 0.f;
+      for (int I = 0; I < 4; ++I) acc[I] = mfma(kf[I][ks], kf[I][ks], acc[I]);
+    // acc[I][i] = k_r . k_c, r = 16I + 4g + i, c = 16I + n16 -> N[r][c] for r > c
+    // (entries with r <= c are never read).
 #pragma unroll
-      for (int q = 0; q < b; ++q) part += cross[4 * b + e][q] * xr[q];
-      tot[e] = b > 0 ? sum_rows(part) : 0.f;
+    for (int I = 0; I < 4; ++I) {
+      const float gc = cb.gam[16 * I + n16];
+      const f32x4 gr = ld4(cb.gam + 16 * I + 4 * g), br = ld4(cb.bet + 16 * I + 4 * g);
+      f32x4 x;
+#pragma unroll
+      for (int i = 0; i < 4; ++i) x[i] = br[i] * exp_le0(fminf(gr[i] - gc, 0.f)) * acc[I][i];
+      *reinterpret_cast<f32x4*>(sm.Nd + I * NDB + n16 * 16 + 4 * g) = x;
     }
-    float x[4];
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int i = 4 * b + e;
-      float acc = tot[e];
-#pragma unroll
-      for (int e2 = 0; e2 < e; ++e2) acc += diag[i][e2] * x[e2];
-      x[e] = i > j ? -acc : (i == j ? 1.f : 0.f);
-    }
-    xr[b] = r == 0 ? x[0] : (r == 1 ? x[1] : (r == 2 ? x[2] : x[3]));
   }
-  const int col = perm(16 * I + j);
-  uint2 hi, lo;
-  split4(f32x4{xr[0], xr[1], xr[2], xr[3]}, hi, lo);
-  const uint32_t h4[4] = {hi.x, hi.x >> 16, hi.y, hi.y >> 16}, l4[4] = {lo.x, lo.x >> 16, lo.y, lo.y >> 16};
+  wave_lds_sync();
+  const int r = g, j = n16;
+  const float* nb = sm.Nd + r * NDB;
+  // All columns first (one round of LDS latency instead of one per step).
+  f32x4 colv[15][4];
+#pragma unroll
+  for (int m = 0; m < 15; ++m)
+#pragma unroll
+    for (int q = (m + 1) / 4; q < 4; ++q) colv[m][q] = ld4(nb + m * 16 + 4 * q);
+  __builtin_amdgcn_sched_barrier(0);
+  float a[16], x[16];
+#pragma unroll
+  for (int m = 0; m < 16; ++m) {
+    x[m] = (m == j) ? 1.f : (m == 0 ? 0.f : -a[m]);
+    if (m < 15) {
+#pragma unroll
+      for (int q = (m + 1) / 4; q < 4; ++q) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int i = 4 * q + e;
+          if (i > m) a[i] = m == 0 ? colv[m][q][e] * x[0] : fmaf(colv[m][q][e], x[m], a[i]);
+        }
+      }
+    }
+  }
+  // rows 16r + i, column 16r + j of T~
+  const int colp = perm(16 * r + j);
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
-    const int row = 16 * I + 4 * q + r;
-    cb.Th[row * TSTR + col] = uint16_t(h4[q]);
-    cb.Tl[row * TSTR + col] = uint16_t(l4[q]);
+    uint2 hi, lo;
+    split4(f32x4{x[4 * q], x[4 * q + 1], x[4 * q + 2], x[4 * q + 3]}, hi, lo);
+    const uint32_t h4[4] = {hi.x, hi.x >> 16, hi.y, hi.y >> 16}, l4[4] = {lo.x, lo.x >> 16, lo.y, lo.y >> 16};
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      cb.Th[(16 * r + 4 * q + e) * TSTR + colp] = uint16_t(h4[e]);
+      cb.Tl[(16 * r + 4 * q + e) * TSTR + colp] = uint16_t(l4[e]);
+    }
   }
 }
 
@@ -570,65 +579,48 @@ __device__ __forceinline__ void producer_loop(PrefillSmem& sm, const PrefillArgs
     // ahead of the consumer wave sharing the SIMD.
     __builtin_amdgcn_s_setprio(1);
 
-    // 2: N tiles (and two P tiles), diagonal blocks of T~
+    // 2: next chunk's K/Q/a/b into registers (staged at the next tick's start);
+    // diagonal blocks of T~ (first producer wave), N and P tiles (the others)
     if (work) {
+      const int64_t ncs = cs + C;
+      if (ncs < s1) producer_prefetch(p, ncs, int(s1 - ncs < C ? s1 - ncs : C), h, hq, hk, pt, f);
       switch (pw) {
-        case 0: {
-          const TileJob jobs[3] = {{0, 0, 0}, {1, 1, 0}, {1, 2, 0}};
-          run_tiles(sm, cb, jobs, p.scale, lane);
+        case 0:
+          diag_blocks(sm, cb, lane);
           break;
-        }
         case 1: {
-          const TileJob jobs[3] = {{0, 1, 1}, {1, 3, 0}, {1, 2, 1}};
-          run_tiles(sm, cb, jobs, p.scale, lane);
+          const TileJob j1[3] = {{1, 1, 0}, {1, 2, 0}, {2, 0, 0}};
+          run_tiles(sm, cb, j1, p.scale, lane);
+          const TileJob j2[3] = {{2, 1, 0}, {2, 1, 1}, {2, 3, 3}};
+          run_tiles(sm, cb, j2, p.scale, lane);
           break;
         }
         case 2: {
-          const TileJob jobs[3] = {{0, 2, 2}, {1, 3, 1}, {1, 3, 2}};
-          run_tiles(sm, cb, jobs, p.scale, lane);
+          const TileJob j1[3] = {{1, 3, 0}, {1, 2, 1}, {2, 2, 0}};
+          run_tiles(sm, cb, j1, p.scale, lane);
+          const TileJob j2[2] = {{2, 2, 1}, {2, 2, 2}};
+          run_tiles(sm, cb, j2, p.scale, lane);
           break;
         }
         default: {
-          const TileJob jobs[3] = {{0, 3, 3}, {2, 3, 3}, {2, 3, 2}};
-          run_tiles(sm, cb, jobs, p.scale, lane);
+          const TileJob j1[3] = {{1, 3, 1}, {1, 3, 2}, {2, 3, 0}};
+          run_tiles(sm, cb, j1, p.scale, lane);
+          const TileJob j2[2] = {{2, 3, 1}, {2, 3, 2}};
+          run_tiles(sm, cb, j2, p.scale, lane);
           break;
         }
       }
-      wave_lds_sync();  // this wave wrote its diagonal block of N
-      solve_diagonal_block(sm, cb, pw, lane);
     }
     lds_barrier();
 
-    // 3: off-diagonal blocks of T~ (last producer wave), remaining P tiles;
-    // next chunk's inputs into registers
+    // 3: off-diagonal blocks of T~ (last producer wave), V
     if (work) {
-      switch (pw) {
-        case 0: {
-          const TileJob jobs[3] = {{2, 0, 0}, {2, 1, 0}, {2, 1, 1}};
-          run_tiles(sm, cb, jobs, p.scale, lane);
-          break;
-        }
-        case 1: {
-          const TileJob jobs[3] = {{2, 2, 0}, {2, 2, 1}, {2, 2, 2}};
-          run_tiles(sm, cb, jobs, p.scale, lane);
-          break;
-        }
-        case 2: {
-          const TileJob jobs[2] = {{2, 3, 0}, {2, 3, 1}};
-          run_tiles(sm, cb, jobs, p.scale, lane);
-          break;
-        }
-        default:
-          solve_offdiagonal(sm, cb, lane);
-          break;
-      }
+      if (pw == 3) solve_offdiagonal(sm, cb, lane);
 #pragma unroll
       for (int it = 0; it < 4; ++it) {
         const int seg = pt + it * NPROD;
         *reinterpret_cast<uint4*>(sm.V + (seg >> 4) * VSTR + 8 * (seg & 15)) = fv[it];
       }
-      const int64_t ncs = cs + C;
-      if (ncs < s1) producer_prefetch(p, ncs, int(s1 - ncs < C ? s1 - ncs : C), h, hq, hk, pt, f);
     }
     __builtin_amdgcn_s_setprio(0);
     lds_barrier();
