@@ -58,6 +58,7 @@ def parse():
     return ap.parse_args()
 
 
+PREFILL_WARM_S = 0.3   # untimed prefill launches before timing (clock ramp-up)
 COPY_BYTES = 1 << 28   # 256 MiB read + 256 MiB written by the calibration copy
 
 
@@ -183,8 +184,17 @@ def bench_prefill(args, torch, binding, workloads, cfg):
         binding.prefill_kernel(p["q"], p["k"], p["v"], p["state"], p["A_log"], p["a"],
                                p["dt_bias"], p["b"], p["cu_seqlens"], p["scale"], out, ns)
 
-    steps = max(3, args.steps // 5)
-    wall, ev_mean, _ = timed_launches(step, steps, min(args.warmup, 2), torch)
+    # Untimed warm-up for at least PREFILL_WARM_S (the GPU leaves its idle clocks
+    # within the first few hundred milliseconds), then `steps` timed launches.
+    steps = max(10, args.steps // 2)
+    t_end = time.perf_counter() + PREFILL_WARM_S
+    nwarm = 0
+    while nwarm < max(args.warmup, 2) or time.perf_counter() < t_end:
+        step(nwarm)
+        nwarm += 1
+        if nwarm % 8 == 0:
+            torch.cuda.synchronize()
+    wall, ev_mean, _ = timed_launches(step, steps, 0, torch)
     flop = HV * T * PREFILL_FLOP_PER_TOKEN_HEAD
     tfs = flop / (ev_mean * 1e-3) / 1e12
     return dict(tokens=T, seqs=N, us=ev_mean * 1e3, tokens_per_s=T / (ev_mean * 1e-3),

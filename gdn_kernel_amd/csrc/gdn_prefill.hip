@@ -60,8 +60,17 @@ constexpr int KSTR = 128;    // bf16 row stride of the K and Q tiles (16-byte sl
 constexpr int VSTR = 144;    // bf16 row stride of the V tile (rows 32 bytes apart modulo 128)
 constexpr int TSTR = 72;     // bf16 row stride of 64-wide tiles (T~, P, N)
 constexpr int NDB = 16 * 16 + 4;  // floats per diagonal N block (column-major; padded by 16 bytes)
-constexpr int NTHREADS = 512;
-constexpr int NPROD = 256;   // producer threads (waves 4-7)
+#ifndef GDN_PREFILL_CONSUMER_WAVES
+#define GDN_PREFILL_CONSUMER_WAVES 4
+#endif
+constexpr int NCW = GDN_PREFILL_CONSUMER_WAVES;  // consumer waves (4 or 8)
+constexpr int VT = 128 / (16 * NCW);             // 16-row state tiles per consumer wave
+constexpr int VW = 16 * VT;                      // state rows per consumer wave
+constexpr int NTHREADS = 64 * (NCW + 4);
+constexpr int NPROD = 256;   // producer threads (the last four waves)
+// The next chunk's K/Q loads go out at the start of the middle producer
+// sub-phase when registers allow (two waves per SIMD), else at the end of the tick.
+constexpr bool kEarlyPrefetch = NCW == 4;
 constexpr int NROWS = C - 16;  // rows of N kept for the off-diagonal solve
 constexpr int kMaxSortedSeqs = 1024;  // longest-first ordering up to this many sequences
 
@@ -335,18 +344,16 @@ __device__ __forceinline__ void run_tiles(PrefillSmem& sm, const ChunkBufs& cb, 
 __device__ __forceinline__ void diag_blocks(PrefillSmem& sm, const ChunkBufs& cb, int lane) {
   const int g = lane >> 4, n16 = lane & 15;
   {
-    uint4 kf[4][4];
-#pragma unroll
-    for (int I = 0; I < 4; ++I)
-#pragma unroll
-      for (int ks = 0; ks < 4; ++ks) kf[I][ks] = frag_kq(cb.K, 16 * I, ks, lane);
     f32x4 acc[4];
 #pragma unroll
-    for (int I = 0; I < 4; ++I) acc[I] = zero4();
+    for (int I = 0; I < 4; ++I) {
+      uint4 kf[4];
 #pragma unroll
-    for (int ks = 0; ks < 4; ++ks)
+      for (int ks = 0; ks < 4; ++ks) kf[ks] = frag_kq(cb.K, 16 * I, ks, lane);
+      acc[I] = zero4();
 #pragma unroll
-      for (int I = 0; I < 4; ++I) acc[I] = mfma(kf[I][ks], kf[I][ks], acc[I]);
+      for (int ks = 0; ks < 4; ++ks) acc[I] = mfma(kf[ks], kf[ks], acc[I]);
+    }
     // acc[I][i] = k_r . k_c, r = 16I + 4g + i, c = 16I + n16 -> N[r][c] for r > c
     // (entries with r <= c are never read).
 #pragma unroll
@@ -362,17 +369,22 @@ __device__ __forceinline__ void diag_blocks(PrefillSmem& sm, const ChunkBufs& cb
   wave_lds_sync();
   const int r = g, j = n16;
   const float* nb = sm.Nd + r * NDB;
-  // All columns first (one round of LDS latency instead of one per step).
+  // Columns are read kColAhead steps ahead of their use.
+  constexpr int kColAhead = NCW == 4 ? 4 : 2;
   f32x4 colv[15][4];
 #pragma unroll
-  for (int m = 0; m < 15; ++m)
+  for (int m = 0; m < kColAhead; ++m)
 #pragma unroll
     for (int q = (m + 1) / 4; q < 4; ++q) colv[m][q] = ld4(nb + m * 16 + 4 * q);
-  __builtin_amdgcn_sched_barrier(0);
   float a[16], x[16];
 #pragma unroll
   for (int m = 0; m < 16; ++m) {
     x[m] = (m == j) ? 1.f : (m == 0 ? 0.f : -a[m]);
+    if (m + kColAhead < 15) {
+#pragma unroll
+      for (int q = (m + kColAhead + 1) / 4; q < 4; ++q)
+        colv[m + kColAhead][q] = ld4(nb + (m + kColAhead) * 16 + 4 * q);
+    }
     if (m < 15) {
 #pragma unroll
       for (int q = (m + 1) / 4; q < 4; ++q) {
@@ -582,31 +594,39 @@ __device__ __forceinline__ void producer_loop(PrefillSmem& sm, const PrefillArgs
     // 2: next chunk's K/Q/a/b into registers (staged at the next tick's start);
     // diagonal blocks of T~ (first producer wave), N and P tiles (the others)
     if (work) {
-      const int64_t ncs = cs + C;
-      if (ncs < s1) producer_prefetch(p, ncs, int(s1 - ncs < C ? s1 - ncs : C), h, hq, hk, pt, f);
+      if (kEarlyPrefetch) {
+        const int64_t ncs = cs + C;
+        if (ncs < s1) producer_prefetch(p, ncs, int(s1 - ncs < C ? s1 - ncs : C), h, hq, hk, pt, f);
+      }
       switch (pw) {
         case 0:
           diag_blocks(sm, cb, lane);
           break;
         case 1: {
-          const TileJob j1[3] = {{1, 1, 0}, {1, 2, 0}, {2, 0, 0}};
+          const TileJob j1[2] = {{1, 1, 0}, {1, 2, 0}};
           run_tiles(sm, cb, j1, p.scale, lane);
-          const TileJob j2[3] = {{2, 1, 0}, {2, 1, 1}, {2, 3, 3}};
+          const TileJob j2[2] = {{2, 0, 0}, {2, 1, 0}};
           run_tiles(sm, cb, j2, p.scale, lane);
+          const TileJob j3[2] = {{2, 1, 1}, {2, 3, 3}};
+          run_tiles(sm, cb, j3, p.scale, lane);
           break;
         }
         case 2: {
-          const TileJob j1[3] = {{1, 3, 0}, {1, 2, 1}, {2, 2, 0}};
+          const TileJob j1[2] = {{1, 3, 0}, {1, 2, 1}};
           run_tiles(sm, cb, j1, p.scale, lane);
-          const TileJob j2[2] = {{2, 2, 1}, {2, 2, 2}};
+          const TileJob j2[2] = {{2, 2, 0}, {2, 2, 1}};
           run_tiles(sm, cb, j2, p.scale, lane);
+          const TileJob j3[1] = {{2, 2, 2}};
+          run_tiles(sm, cb, j3, p.scale, lane);
           break;
         }
         default: {
-          const TileJob j1[3] = {{1, 3, 1}, {1, 3, 2}, {2, 3, 0}};
+          const TileJob j1[2] = {{1, 3, 1}, {1, 3, 2}};
           run_tiles(sm, cb, j1, p.scale, lane);
-          const TileJob j2[2] = {{2, 3, 1}, {2, 3, 2}};
+          const TileJob j2[2] = {{2, 3, 0}, {2, 3, 1}};
           run_tiles(sm, cb, j2, p.scale, lane);
+          const TileJob j3[1] = {{2, 3, 2}};
+          run_tiles(sm, cb, j3, p.scale, lane);
           break;
         }
       }
@@ -621,6 +641,10 @@ __device__ __forceinline__ void producer_loop(PrefillSmem& sm, const PrefillArgs
         const int seg = pt + it * NPROD;
         *reinterpret_cast<uint4*>(sm.V + (seg >> 4) * VSTR + 8 * (seg & 15)) = fv[it];
       }
+      if (!kEarlyPrefetch) {
+        const int64_t ncs = cs + C;
+        if (ncs < s1) producer_prefetch(p, ncs, int(s1 - ncs < C ? s1 - ncs : C), h, hq, hk, pt, f);
+      }
     }
     __builtin_amdgcn_s_setprio(0);
     lds_barrier();
@@ -633,23 +657,23 @@ __device__ __forceinline__ void producer_loop(PrefillSmem& sm, const PrefillArgs
 
 // Xk = K S^T (rows c, cols v) with S as hi/lo B operands, and Xq = (Q S^T)^T
 // (rows v, cols c) with S's hi part as the A operand (output-only product).
-__device__ __forceinline__ void retrieve(const ChunkBufs& cb, const f32x4 (&S)[2][8], f32x4 (&Xk)[4][2],
-                                         f32x4 (&Xq)[2][4], int lane) {
+__device__ __forceinline__ void retrieve(const ChunkBufs& cb, const f32x4 (&S)[VT][8], f32x4 (&Xk)[4][VT],
+                                         f32x4 (&Xq)[VT][4], int lane) {
 #pragma unroll
   for (int ct = 0; ct < 4; ++ct)
 #pragma unroll
-    for (int vt = 0; vt < 2; ++vt) Xk[ct][vt] = Xq[vt][ct] = zero4();
+    for (int vt = 0; vt < VT; ++vt) Xk[ct][vt] = Xq[vt][ct] = zero4();
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) {
-    uint4 Sh[2], Sl[2];
+    uint4 Sh[VT], Sl[VT];
 #pragma unroll
-    for (int vt = 0; vt < 2; ++vt) split_pack(S[vt][2 * ks], S[vt][2 * ks + 1], Sh[vt], Sl[vt]);
+    for (int vt = 0; vt < VT; ++vt) split_pack(S[vt][2 * ks], S[vt][2 * ks + 1], Sh[vt], Sl[vt]);
 #pragma unroll
     for (int ct = 0; ct < 4; ++ct) {
       const uint4 ak = frag_kq(cb.K, 16 * ct, ks, lane);
       const uint4 bq = frag_kq(cb.Q, 16 * ct, ks, lane);
 #pragma unroll
-      for (int vt = 0; vt < 2; ++vt) {
+      for (int vt = 0; vt < VT; ++vt) {
         Xk[ct][vt] = mfma(ak, Sh[vt], Xk[ct][vt]);
         Xk[ct][vt] = mfma(ak, Sl[vt], Xk[ct][vt]);
         Xq[vt][ct] = mfma(Sh[vt], bq, Xq[vt][ct]);
@@ -661,7 +685,7 @@ __device__ __forceinline__ void retrieve(const ChunkBufs& cb, const f32x4 (&S)[2
 // The consumer loop: tick t (>= 1) advances the state through chunk t-1 from the
 // buffers of parity (t-1) & 1.  Three barriers per tick, matching the producers.
 __device__ __forceinline__ void consumer_loop(PrefillSmem& sm, const PrefillArgs& p, int64_t s0, int64_t s1,
-                                              int nchunks, int h, int wave, int lane0, f32x4 (&S)[2][8]) {
+                                              int nchunks, int h, int wave, int lane0, f32x4 (&S)[VT][8]) {
   lds_barrier();  // LDS clearing done (matched by the producers)
   // Tick 0 only fills the pipeline.
   lds_barrier();
@@ -680,46 +704,46 @@ __device__ __forceinline__ void consumer_loop(PrefillSmem& sm, const PrefillArgs
     const ChunkBufs cb = chunk_bufs(sm, (t - 1) & 1);
 
     // 1: X = K S^T, (Q S^T)^T
-    f32x4 Xk[4][2], Xq[2][4];
+    f32x4 Xk[4][VT], Xq[VT][4];
     retrieve(cb, S, Xk, Xq, lane);
     lds_barrier();
 
     // 2: Y, v_new, output
-    // Y = beta (V - e^gamma X); element (c = 16ct + 4g + i, v = 32w + 16vt + n16).
+    // Y = beta (V - e^gamma X); element (c = 16ct + 4g + i, v = VW w + 16vt + n16).
 #pragma unroll
     for (int ct = 0; ct < 4; ++ct) {
       const float4 bc = *reinterpret_cast<const float4*>(cb.bet + 16 * ct + 4 * g);
       const float4 ec = *reinterpret_cast<const float4*>(cb.eg + 16 * ct + 4 * g);
       const float b4[4] = {bc.x, bc.y, bc.z, bc.w}, e4[4] = {ec.x, ec.y, ec.z, ec.w};
 #pragma unroll
-      for (int vt = 0; vt < 2; ++vt) {
-        // V rows 16ct + 4g .. +3 of column 32w + 16vt + n16 (zero past the chunk end)
-        const uint2 vv = col4_tr_plain(sm.V, VSTR, 16 * ct, 32 * wave + 16 * vt, lane);
+      for (int vt = 0; vt < VT; ++vt) {
+        // V rows 16ct + 4g .. +3 of column VW w + 16vt + n16 (zero past the chunk end)
+        const uint2 vv = col4_tr_plain(sm.V, VSTR, 16 * ct, VW * wave + 16 * vt, lane);
         const float vf[4] = {bf16lo_f32(vv.x), bf16hi_f32(vv.x), bf16lo_f32(vv.y), bf16hi_f32(vv.y)};
 #pragma unroll
         for (int i = 0; i < 4; ++i) Xk[ct][vt][i] = b4[i] * (vf[i] - e4[i] * Xk[ct][vt][i]);
       }
       const float ecn = cb.eg[16 * ct + n16] * p.scale;  // scale e^gamma of output column c = 16ct + n16
 #pragma unroll
-      for (int vt = 0; vt < 2; ++vt) Xq[vt][ct] = Xq[vt][ct] * ecn;
+      for (int vt = 0; vt < VT; ++vt) Xq[vt][ct] = Xq[vt][ct] * ecn;
     }
     // v_new = T~ Y (contraction over the rows of Y in blocks js; T~ is lower triangular).
-    uint4 Yh[2][2], Yl[2][2];
+    uint4 Yh[VT][2], Yl[VT][2];
 #pragma unroll
-    for (int vt = 0; vt < 2; ++vt)
+    for (int vt = 0; vt < VT; ++vt)
 #pragma unroll
       for (int js = 0; js < 2; ++js) split_pack(Xk[2 * js][vt], Xk[2 * js + 1][vt], Yh[vt][js], Yl[vt][js]);
-    f32x4 Vn[4][2];
+    f32x4 Vn[4][VT];
 #pragma unroll
     for (int ct = 0; ct < 4; ++ct) {
 #pragma unroll
-      for (int vt = 0; vt < 2; ++vt) Vn[ct][vt] = zero4();
+      for (int vt = 0; vt < VT; ++vt) Vn[ct][vt] = zero4();
 #pragma unroll
       for (int js = 0; js <= (ct >> 1); ++js) {
         const uint4 th = frag(cb.Th, TSTR, 16 * ct, js, lane);
         const uint4 tl = frag(cb.Tl, TSTR, 16 * ct, js, lane);
 #pragma unroll
-        for (int vt = 0; vt < 2; ++vt) {
+        for (int vt = 0; vt < VT; ++vt) {
           Vn[ct][vt] = mfma(th, Yh[vt][js], Vn[ct][vt]);
           Vn[ct][vt] = mfma(th, Yl[vt][js], Vn[ct][vt]);
           Vn[ct][vt] = mfma(tl, Yh[vt][js], Vn[ct][vt]);
@@ -729,23 +753,23 @@ __device__ __forceinline__ void consumer_loop(PrefillSmem& sm, const PrefillArgs
     // o^T = scale e^gamma (S Q^T) + v_new^T (scale P)^T (rows v, cols c); P is lower triangular.
 #pragma unroll
     for (int js = 0; js < 2; ++js) {
-      uint4 vb[2];
+      uint4 vb[VT];
 #pragma unroll
-      for (int vt = 0; vt < 2; ++vt) vb[vt] = pack_hi(Vn[2 * js][vt], Vn[2 * js + 1][vt]);
+      for (int vt = 0; vt < VT; ++vt) vb[vt] = pack_hi(Vn[2 * js][vt], Vn[2 * js + 1][vt]);
 #pragma unroll
       for (int ct = 2 * js; ct < 4; ++ct) {
         const uint4 pq = frag(cb.P, TSTR, 16 * ct, js, lane);
 #pragma unroll
-        for (int vt = 0; vt < 2; ++vt) Xq[vt][ct] = mfma(vb[vt], pq, Xq[vt][ct]);
+        for (int vt = 0; vt < VT; ++vt) Xq[vt][ct] = mfma(vb[vt], pq, Xq[vt][ct]);
       }
     }
-    // Lane holds o[c = 16ct + n16][v = 32w + 16vt + 4g .. +3]: one 8-byte store each.
-    uint16_t* obase = p.out + cs * vstride + (int64_t(h) * D + 32 * wave + 4 * g);
+    // Lane holds o[c = 16ct + n16][v = VW w + 16vt + 4g .. +3]: one 8-byte store each.
+    uint16_t* obase = p.out + cs * vstride + (int64_t(h) * D + VW * wave + 4 * g);
 #pragma unroll
     for (int ct = 0; ct < 4; ++ct) {
       if (16 * ct + n16 < clen) {
 #pragma unroll
-        for (int vt = 0; vt < 2; ++vt) {
+        for (int vt = 0; vt < VT; ++vt) {
           const f32x4& o = Xq[vt][ct];
           *reinterpret_cast<uint2*>(obase + orow[ct] + 16 * vt) = uint2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
         }
@@ -755,24 +779,24 @@ __device__ __forceinline__ void consumer_loop(PrefillSmem& sm, const PrefillArgs
 
     // 3: S = e^{gamma_last} S + sum_c K[c]^T (d_c v_new[c]),  d_c = e^{gamma_last - gamma_c}
     const float dlast = cb.eg[clen - 1];
-    uint4 Uh[2][2], Ul[2][2];
+    uint4 Uh[VT][2], Ul[VT][2];
 #pragma unroll
     for (int js = 0; js < 2; ++js) {
       const float4 d0 = *reinterpret_cast<const float4*>(cb.dd + 32 * js + 4 * g);
       const float4 d1 = *reinterpret_cast<const float4*>(cb.dd + 32 * js + 16 + 4 * g);
       const f32x4 e0 = {d0.x, d0.y, d0.z, d0.w}, e1 = {d1.x, d1.y, d1.z, d1.w};
 #pragma unroll
-      for (int vt = 0; vt < 2; ++vt) split_pack(Vn[2 * js][vt] * e0, Vn[2 * js + 1][vt] * e1, Uh[vt][js], Ul[vt][js]);
+      for (int vt = 0; vt < VT; ++vt) split_pack(Vn[2 * js][vt] * e0, Vn[2 * js + 1][vt] * e1, Uh[vt][js], Ul[vt][js]);
     }
 #pragma unroll
     for (int kt = 0; kt < 8; ++kt) {
 #pragma unroll
-      for (int vt = 0; vt < 2; ++vt) S[vt][kt] = S[vt][kt] * dlast;
+      for (int vt = 0; vt < VT; ++vt) S[vt][kt] = S[vt][kt] * dlast;
 #pragma unroll
       for (int js = 0; js < 2; ++js) {
         const uint4 ak = frag_tr_k(cb.K, 32 * js, 16 * kt, lane);
 #pragma unroll
-        for (int vt = 0; vt < 2; ++vt) {
+        for (int vt = 0; vt < VT; ++vt) {
           S[vt][kt] = mfma(ak, Uh[vt][js], S[vt][kt]);
           S[vt][kt] = mfma(ak, Ul[vt][js], S[vt][kt]);
         }
@@ -844,18 +868,18 @@ __global__ __launch_bounds__(NTHREADS) void gdn_prefill_kernel(PrefillArgs p) {
     }
   }
 
-  if (wave >= 4) {
-    if (nchunks > 0) producer_loop(sm, p, s0, s1, nchunks, h, hq, hk, wave - 4, lane0);
+  if (wave >= NCW) {
+    if (nchunks > 0) producer_loop(sm, p, s0, s1, nchunks, h, hq, hk, wave - NCW, lane0);
     return;
   }
 
-  // Consumer state slab: rows v = 32*wave + 16*vt + n16, cols k = 16*kt + 4g + i.
+  // Consumer state slab: rows v = VW*wave + 16*vt + n16, cols k = 16*kt + 4g + i.
   const int64_t state_head = (int64_t(seq) * p.Hv + h) * D * D;
   const int g = lane0 >> 4, n16 = lane0 & 15;
-  f32x4 S[2][8];
+  f32x4 S[VT][8];
 #pragma unroll
-  for (int vt = 0; vt < 2; ++vt) {
-    const int v = 32 * wave + 16 * vt + n16;
+  for (int vt = 0; vt < VT; ++vt) {
+    const int v = VW * wave + 16 * vt + n16;
 #pragma unroll
     for (int kt = 0; kt < 8; ++kt) {
       if (p.state) {
@@ -871,8 +895,8 @@ __global__ __launch_bounds__(NTHREADS) void gdn_prefill_kernel(PrefillArgs p) {
   // Final state (for an empty sequence: the initial state, or zeros).
   if (nchunks > 0 || p.state != p.new_state) {
 #pragma unroll
-    for (int vt = 0; vt < 2; ++vt) {
-      const int v = 32 * wave + 16 * vt + n16;
+    for (int vt = 0; vt < VT; ++vt) {
+      const int v = VW * wave + 16 * vt + n16;
 #pragma unroll
       for (int kt = 0; kt < 8; ++kt) {
         const f32x4 x = S[vt][kt];
