@@ -89,6 +89,7 @@ struct __align__(16) PrefillSmem {
   float eg[2][C];             // e^{gamma_c}
   float dd[2][C];             // e^{gamma_last - gamma_c}
   int seq;                    // sequence handled by this workgroup
+  int sync[8];                // role hand-off counters (kReady, kVFree, kConsumed, kPPhase, kAbort)
 };
 
 constexpr float kLog2e = 1.4426950408889634f;
@@ -237,6 +238,36 @@ __device__ __forceinline__ void wave_lds_sync() {
 // between the waves of a workgroup here).
 __device__ __forceinline__ void lds_barrier() {
   asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
+}
+
+// Hand-off between the two roles: monotonically increasing LDS counters.  A wave
+// signals by adding 1 after all its earlier LDS accesses completed (release); a
+// waiter polls until the count reaches its target (acquire).
+enum SyncCounter { kReady = 0, kVFree = 1, kConsumed = 2, kPPhase = 3, kAbort = 4 };
+constexpr int kSpinLimit = 1 << 20;  // polls (about 70 ms) before a wait gives up
+
+__device__ __forceinline__ void signal_count(PrefillSmem& sm, int which, int lane) {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  if (lane == 0) __hip_atomic_fetch_add(&sm.sync[which], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+}
+
+// Waits until counter `which` reaches `target`.  Every wait is bounded: if one
+// ever gives up (which only a logic error could cause), it raises kAbort and all
+// later waits return at once, so the workgroup still finishes (with wrong
+// results) instead of hanging.
+__device__ __forceinline__ void wait_count(PrefillSmem& sm, int which, int target) {
+  if (__hip_atomic_load(&sm.sync[which], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < target) {
+    for (int it = 0;; ++it) {
+      __builtin_amdgcn_s_sleep(2);
+      if (__hip_atomic_load(&sm.sync[which], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= target) break;
+      if (__hip_atomic_load(&sm.sync[kAbort], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != 0) break;
+      if (it >= kSpinLimit) {
+        __hip_atomic_store(&sm.sync[kAbort], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        break;
+      }
+    }
+  }
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 }
 
 // The parity-selected LDS buffers of one chunk.
@@ -533,8 +564,10 @@ __device__ __forceinline__ void producer_prefetch(const PrefillArgs& p, int64_t 
   }
 }
 
-// The producer loop: tick t prepares chunk t into the buffers of parity t & 1.
-// Three barriers per tick, matching the consumer loop.
+// The producer loop: chunk t is prepared into the buffers of parity t & 1 once
+// the consumers are done with chunk t - 2 (same parity).  The four producer waves
+// meet twice per chunk (after staging; after the tiles and diagonal blocks) on
+// their own counter; the chunk is handed over when all four are done.
 __device__ __forceinline__ void producer_loop(PrefillSmem& sm, const PrefillArgs& p, int64_t s0, int64_t s1,
                                               int nchunks, int h, int hq, int hk, int pw, int lane0) {
   const int pt = pw * 64 + lane0;
@@ -543,17 +576,17 @@ __device__ __forceinline__ void producer_loop(PrefillSmem& sm, const PrefillArgs
   ProducerPrefetch f;
   uint4 fv[4];
   producer_prefetch(p, s0, int(s1 - s0 < C ? s1 - s0 : C), h, hq, hk, pt, f);
-  lds_barrier();  // LDS clearing done (matched by the consumers)
 
-  for (int t = 0; t <= nchunks; ++t) {
+  for (int t = 0; t < nchunks; ++t) {
     // The lane index is re-materialised opaquely each tick so that lane-dependent
     // LDS addresses are recomputed in the loop rather than hoisted and spilled.
     int lane = lane0;
     asm volatile("" : "+v"(lane));
-    const bool work = t < nchunks;
+    constexpr bool work = true;
     const int64_t cs = s0 + int64_t(t) * C;
-    const int clen = work ? int(s1 - cs < C ? s1 - cs : C) : 0;
+    const int clen = int(s1 - cs < C ? s1 - cs : C);
     const ChunkBufs cb = chunk_bufs(sm, t & 1);
+    if (t >= 2) wait_count(sm, kConsumed, 4 * (t - 1));  // chunk t - 2 consumed
 
     // 1: stage K/Q (permuted columns), gates
     if (work) {
@@ -586,9 +619,10 @@ __device__ __forceinline__ void producer_loop(PrefillSmem& sm, const PrefillArgs
         if (c < clen) fv[it] = *reinterpret_cast<const uint4*>(p.v + ((cs + c) * p.Hv + h) * D + 8 * sg);
       }
     }
-    lds_barrier();
-    // Sub-phases 2 and 3 of the producers are the longer ones: their waves go
-    // ahead of the consumer wave sharing the SIMD.
+    signal_count(sm, kPPhase, lane);
+    wait_count(sm, kPPhase, 4 * (2 * t + 1));  // all of K/Q/gates staged
+    // The rest of the chunk is the longer chain: producer waves go ahead of the
+    // consumer wave sharing the SIMD.
     __builtin_amdgcn_s_setprio(1);
 
     // 2: next chunk's K/Q/a/b into registers (staged at the next tick's start);
@@ -631,11 +665,14 @@ __device__ __forceinline__ void producer_loop(PrefillSmem& sm, const PrefillArgs
         }
       }
     }
-    lds_barrier();
+    signal_count(sm, kPPhase, lane);
+    wait_count(sm, kPPhase, 4 * (2 * t + 2));  // diagonal blocks and N tiles done
 
-    // 3: off-diagonal blocks of T~ (last producer wave), V
+    // 3: off-diagonal blocks of T~ (last producer wave), V once the consumers have
+    // read the previous chunk's
     if (work) {
       if (pw == 3) solve_offdiagonal(sm, cb, lane);
+      if (t >= 1) wait_count(sm, kVFree, 4 * t);
 #pragma unroll
       for (int it = 0; it < 4; ++it) {
         const int seg = pt + it * NPROD;
@@ -647,7 +684,7 @@ __device__ __forceinline__ void producer_loop(PrefillSmem& sm, const PrefillArgs
       }
     }
     __builtin_amdgcn_s_setprio(0);
-    lds_barrier();
+    signal_count(sm, kReady, lane);
   }
 }
 
@@ -682,15 +719,10 @@ __device__ __forceinline__ void retrieve(const ChunkBufs& cb, const f32x4 (&S)[V
   }
 }
 
-// The consumer loop: tick t (>= 1) advances the state through chunk t-1 from the
-// buffers of parity (t-1) & 1.  Three barriers per tick, matching the producers.
+// The consumer loop: iteration t (>= 1) advances the state through chunk t-1
+// from the buffers of parity (t-1) & 1, once the producers have handed it over.
 __device__ __forceinline__ void consumer_loop(PrefillSmem& sm, const PrefillArgs& p, int64_t s0, int64_t s1,
                                               int nchunks, int h, int wave, int lane0, f32x4 (&S)[VT][8]) {
-  lds_barrier();  // LDS clearing done (matched by the producers)
-  // Tick 0 only fills the pipeline.
-  lds_barrier();
-  lds_barrier();
-  lds_barrier();
   const int64_t vstride = int64_t(p.Hv) * D;
   int orow[4];  // element offset of output row 16ct + lane%16 from the chunk start
 #pragma unroll
@@ -702,11 +734,11 @@ __device__ __forceinline__ void consumer_loop(PrefillSmem& sm, const PrefillArgs
     const int64_t cs = s0 + int64_t(t - 1) * C;
     const int clen = int(s1 - cs < C ? s1 - cs : C);
     const ChunkBufs cb = chunk_bufs(sm, (t - 1) & 1);
+    wait_count(sm, kReady, 4 * t);  // chunk t - 1 prepared
 
     // 1: X = K S^T, (Q S^T)^T
     f32x4 Xk[4][VT], Xq[VT][4];
     retrieve(cb, S, Xk, Xq, lane);
-    lds_barrier();
 
     // 2: Y, v_new, output
     // Y = beta (V - e^gamma X); element (c = 16ct + 4g + i, v = VW w + 16vt + n16).
@@ -727,6 +759,7 @@ __device__ __forceinline__ void consumer_loop(PrefillSmem& sm, const PrefillArgs
 #pragma unroll
       for (int vt = 0; vt < VT; ++vt) Xq[vt][ct] = Xq[vt][ct] * ecn;
     }
+    signal_count(sm, kVFree, lane);  // V of this chunk read
     // v_new = T~ Y (contraction over the rows of Y in blocks js; T~ is lower triangular).
     uint4 Yh[VT][2], Yl[VT][2];
 #pragma unroll
@@ -775,7 +808,6 @@ __device__ __forceinline__ void consumer_loop(PrefillSmem& sm, const PrefillArgs
         }
       }
     }
-    lds_barrier();
 
     // 3: S = e^{gamma_last} S + sum_c K[c]^T (d_c v_new[c]),  d_c = e^{gamma_last - gamma_c}
     const float dlast = cb.eg[clen - 1];
@@ -802,7 +834,7 @@ __device__ __forceinline__ void consumer_loop(PrefillSmem& sm, const PrefillArgs
         }
       }
     }
-    lds_barrier();
+    signal_count(sm, kConsumed, lane);  // buffers of this chunk no longer read
   }
 }
 
@@ -866,7 +898,9 @@ __global__ __launch_bounds__(NTHREADS) void gdn_prefill_kernel(PrefillArgs p) {
         reinterpret_cast<uint4*>(sm.Nl)[e] = z;
       }
     }
+    if (tid < 8) sm.sync[tid] = 0;
   }
+  __syncthreads();  // cleared LDS and counters visible to both roles
 
   if (wave >= NCW) {
     if (nchunks > 0) producer_loop(sm, p, s0, s1, nchunks, h, hq, hk, wave - NCW, lane0);
