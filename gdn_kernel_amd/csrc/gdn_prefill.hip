@@ -7,10 +7,12 @@
 //     P = tril(Gamma QK^T), and T~ = (I + N)^-1;
 //   * consumer waves 0-3 meanwhile advance the state through chunk t-1.
 // Every LDS buffer a consumer reads (K, Q, T~, P, gates) is double-buffered by
-// chunk parity, so a tick is three workgroup barriers with both stages working
-// in between.  The fp32 state never leaves the register file: consumer wave w
-// owns state rows v in [32w, 32w+32) as MFMA accumulators (16x16 tiles of S^T;
-// lane = (k-group g = lane/16, column n = lane%16) holds S[v][k..k+3]).
+// chunk parity (V is single-buffered and rewritten only after it was read).
+// The roles hand chunks over through LDS counters, so each runs its own chain
+// and neither waits for the other's sub-steps.  The fp32 state never leaves the
+// register file: consumer wave w owns state rows v in [VW w, VW w + VW) (VW = 32
+// with the default four consumer waves) as MFMA accumulators (16x16 tiles of
+// S^T; lane = (k-group g = lane/16, column n = lane%16) holds S[v][k..k+3]).
 //
 // Per chunk (positions >= clen are zero-padded: K = Q = V = 0, beta = 0 and
 // log-gate 0, as kernel_prefill.cu:102-114, 125-132 pads them):
@@ -231,13 +233,6 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
-// Workgroup barrier ordering LDS only: waits for this wave's LDS operations,
-// not for its outstanding global loads/stores (no global memory is shared
-// between the waves of a workgroup here).
-__device__ __forceinline__ void lds_barrier() {
-  asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory");
 }
 
 // Hand-off between the two roles: monotonically increasing LDS counters.  A wave
