@@ -91,7 +91,7 @@ struct __align__(16) PrefillSmem {
   float eg[2][C];             // e^{gamma_c}
   float dd[2][C];             // e^{gamma_last - gamma_c}
   int seq;                    // sequence handled by this workgroup
-  int sync[8];                // role hand-off counters (kReady, kVFree, kConsumed, kPPhase, kAbort)
+  int sync[8];                // hand-off counters (kReady, kVFree, kConsumed, kPPhase, kAbort, kDiagN)
 };
 
 constexpr float kLog2e = 1.4426950408889634f;
@@ -238,7 +238,7 @@ __device__ __forceinline__ void wave_lds_sync() {
 // Hand-off between the two roles: monotonically increasing LDS counters.  A wave
 // signals by adding 1 after all its earlier LDS accesses completed (release); a
 // waiter polls until the count reaches its target (acquire).
-enum SyncCounter { kReady = 0, kVFree = 1, kConsumed = 2, kPPhase = 3, kAbort = 4 };
+enum SyncCounter { kReady = 0, kVFree = 1, kConsumed = 2, kPPhase = 3, kAbort = 4, kDiagN = 5 };
 constexpr int kSpinLimit = 1 << 20;  // polls (about 70 ms) before a wait gives up
 
 __device__ __forceinline__ void signal_count(PrefillSmem& sm, int which, int lane) {
@@ -360,19 +360,21 @@ __device__ __forceinline__ void run_tiles(PrefillSmem& sm, const ChunkBufs& cb, 
   for (int t = 0; t < NJ; ++t) tile_epilogue(sm, cb, jobs[t], acc[t], scale, lane);
 }
 
-// The four diagonal blocks of T~, D_I = (I + N_II)^-1, on one wavefront.
-// The tiles K_I K_I^T give N_II (scaled as in the off-diagonal epilogue), stored
-// column-major; then lane (r, j) = (lane/16, lane%16) inverts block r, column j,
+// The four diagonal blocks of T~, D_I = (I + N_II)^-1.  diag_tiles forms N_II
+// from the tiles K_I K_I^T (scaled as in the off-diagonal epilogue) for blocks
+// I0 .. I1-1, stored column-major; diag_solve (one wavefront, all four blocks)
+// then has lane (r, j) = (lane/16, lane%16) invert block r, column j,
 // x = D_r[:, j], by right-looking forward substitution:
 //   x_m = delta_mj - a_m,  a_i += N[i][m] x_m  for i > m
 // (for m < j every term is zero, so x_m = 0 there).  The column of N needed at
 // step m is one broadcast read per four rows; no cross-lane traffic.
-__device__ __forceinline__ void diag_blocks(PrefillSmem& sm, const ChunkBufs& cb, int lane) {
+template <int I0, int I1>
+__device__ __forceinline__ void diag_tiles(PrefillSmem& sm, const ChunkBufs& cb, int lane) {
   const int g = lane >> 4, n16 = lane & 15;
   {
     f32x4 acc[4];
 #pragma unroll
-    for (int I = 0; I < 4; ++I) {
+    for (int I = I0; I < I1; ++I) {
       uint4 kf[4];
 #pragma unroll
       for (int ks = 0; ks < 4; ++ks) kf[ks] = frag_kq(cb.K, 16 * I, ks, lane);
@@ -383,7 +385,7 @@ __device__ __forceinline__ void diag_blocks(PrefillSmem& sm, const ChunkBufs& cb
     // acc[I][i] = k_r . k_c, r = 16I + 4g + i, c = 16I + n16 -> N[r][c] for r > c
     // (entries with r <= c are never read).
 #pragma unroll
-    for (int I = 0; I < 4; ++I) {
+    for (int I = I0; I < I1; ++I) {
       const float gc = cb.gam[16 * I + n16];
       const f32x4 gr = ld4(cb.gam + 16 * I + 4 * g), br = ld4(cb.bet + 16 * I + 4 * g);
       f32x4 x;
@@ -392,8 +394,10 @@ __device__ __forceinline__ void diag_blocks(PrefillSmem& sm, const ChunkBufs& cb
       *reinterpret_cast<f32x4*>(sm.Nd + I * NDB + n16 * 16 + 4 * g) = x;
     }
   }
-  wave_lds_sync();
-  const int r = g, j = n16;
+}
+
+__device__ __forceinline__ void diag_solve(PrefillSmem& sm, const ChunkBufs& cb, int lane) {
+  const int r = lane >> 4, j = lane & 15;
   const float* nb = sm.Nd + r * NDB;
   // Columns are read kColAhead steps ahead of their use.
   constexpr int kColAhead = NCW == 4 ? 4 : 2;
@@ -620,42 +624,41 @@ __device__ __forceinline__ void producer_loop(PrefillSmem& sm, const PrefillArgs
     // consumer wave sharing the SIMD.
     __builtin_amdgcn_s_setprio(1);
 
-    // 2: next chunk's K/Q/a/b into registers (staged at the next tick's start);
-    // diagonal blocks of T~ (first producer wave), N and P tiles (the others)
+    // 2: next chunk's K/Q/a/b into registers (staged at the next chunk's start);
+    // diagonal blocks of T~ (first producer wave), N tiles (the others)
     if (work) {
       if (kEarlyPrefetch) {
         const int64_t ncs = cs + C;
         if (ncs < s1) producer_prefetch(p, ncs, int(s1 - ncs < C ? s1 - ncs : C), h, hq, hk, pt, f);
       }
+      // The diagonal N tiles come first (the solve waits for them), then the
+      // off-diagonal N tiles; the P tiles wait for the last sub-phase.
       switch (pw) {
         case 0:
-          diag_blocks(sm, cb, lane);
+          diag_tiles<0, 1>(sm, cb, lane);
+          signal_count(sm, kDiagN, lane);
+          wait_count(sm, kDiagN, 4 * (t + 1));
+          diag_solve(sm, cb, lane);
           break;
         case 1: {
+          diag_tiles<1, 2>(sm, cb, lane);
+          signal_count(sm, kDiagN, lane);
           const TileJob j1[2] = {{1, 1, 0}, {1, 2, 0}};
           run_tiles(sm, cb, j1, p.scale, lane);
-          const TileJob j2[2] = {{2, 0, 0}, {2, 1, 0}};
-          run_tiles(sm, cb, j2, p.scale, lane);
-          const TileJob j3[2] = {{2, 1, 1}, {2, 3, 3}};
-          run_tiles(sm, cb, j3, p.scale, lane);
           break;
         }
         case 2: {
+          diag_tiles<2, 3>(sm, cb, lane);
+          signal_count(sm, kDiagN, lane);
           const TileJob j1[2] = {{1, 3, 0}, {1, 2, 1}};
           run_tiles(sm, cb, j1, p.scale, lane);
-          const TileJob j2[2] = {{2, 2, 0}, {2, 2, 1}};
-          run_tiles(sm, cb, j2, p.scale, lane);
-          const TileJob j3[1] = {{2, 2, 2}};
-          run_tiles(sm, cb, j3, p.scale, lane);
           break;
         }
         default: {
+          diag_tiles<3, 4>(sm, cb, lane);
+          signal_count(sm, kDiagN, lane);
           const TileJob j1[2] = {{1, 3, 1}, {1, 3, 2}};
           run_tiles(sm, cb, j1, p.scale, lane);
-          const TileJob j2[2] = {{2, 3, 0}, {2, 3, 1}};
-          run_tiles(sm, cb, j2, p.scale, lane);
-          const TileJob j3[1] = {{2, 3, 2}};
-          run_tiles(sm, cb, j3, p.scale, lane);
           break;
         }
       }
@@ -663,10 +666,35 @@ __device__ __forceinline__ void producer_loop(PrefillSmem& sm, const PrefillArgs
     signal_count(sm, kPPhase, lane);
     wait_count(sm, kPPhase, 4 * (2 * t + 2));  // diagonal blocks and N tiles done
 
-    // 3: off-diagonal blocks of T~ (last producer wave), V once the consumers have
-    // read the previous chunk's
+    // 3: off-diagonal blocks of T~ (last producer wave), P tiles (the others), V
+    // once the consumers have read the previous chunk's
     if (work) {
-      if (pw == 3) solve_offdiagonal(sm, cb, lane);
+      switch (pw) {
+        case 0: {
+          const TileJob j1[2] = {{2, 0, 0}, {2, 1, 0}};
+          run_tiles(sm, cb, j1, p.scale, lane);
+          const TileJob j2[2] = {{2, 1, 1}, {2, 2, 0}};
+          run_tiles(sm, cb, j2, p.scale, lane);
+          break;
+        }
+        case 1: {
+          const TileJob j1[2] = {{2, 2, 1}, {2, 2, 2}};
+          run_tiles(sm, cb, j1, p.scale, lane);
+          const TileJob j2[1] = {{2, 3, 0}};
+          run_tiles(sm, cb, j2, p.scale, lane);
+          break;
+        }
+        case 2: {
+          const TileJob j1[2] = {{2, 3, 1}, {2, 3, 2}};
+          run_tiles(sm, cb, j1, p.scale, lane);
+          const TileJob j2[1] = {{2, 3, 3}};
+          run_tiles(sm, cb, j2, p.scale, lane);
+          break;
+        }
+        default:
+          solve_offdiagonal(sm, cb, lane);
+          break;
+      }
       if (t >= 1) wait_count(sm, kVFree, 4 * t);
 #pragma unroll
       for (int it = 0; it < 4; ++it) {
