@@ -239,7 +239,7 @@ __device__ __forceinline__ void wave_lds_sync() {
 // signals by adding 1 after all its earlier LDS accesses completed (release); a
 // waiter polls until the count reaches its target (acquire).
 enum SyncCounter { kReady = 0, kVFree = 1, kConsumed = 2, kPPhase = 3, kAbort = 4, kDiagN = 5 };
-constexpr int kSpinLimit = 1 << 20;  // polls (about 70 ms) before a wait gives up
+constexpr int kSpinLimit = 1 << 21;  // polls (about 70 ms) before a wait gives up
 
 __device__ __forceinline__ void signal_count(PrefillSmem& sm, int which, int lane) {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
@@ -253,7 +253,7 @@ __device__ __forceinline__ void signal_count(PrefillSmem& sm, int which, int lan
 __device__ __forceinline__ void wait_count(PrefillSmem& sm, int which, int target) {
   if (__hip_atomic_load(&sm.sync[which], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < target) {
     for (int it = 0;; ++it) {
-      __builtin_amdgcn_s_sleep(2);
+      __builtin_amdgcn_s_sleep(1);
       if (__hip_atomic_load(&sm.sync[which], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= target) break;
       if (__hip_atomic_load(&sm.sync[kAbort], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != 0) break;
       if (it >= kSpinLimit) {
