@@ -59,6 +59,7 @@ def parse():
 
 
 PREFILL_WARM_S = 0.3   # untimed prefill launches before timing (clock ramp-up)
+PREFILL_CPU_TOKENS = 1024  # CPU prefill baseline sample (tokens of config 4's sequence 0)
 COPY_BYTES = 1 << 28   # 256 MiB read + 256 MiB written by the calibration copy
 
 
@@ -237,6 +238,34 @@ def cpu_baseline(seconds, workloads):
             "cpu_model": cpu}
 
 
+def cpu_baseline_prefill(seconds, workloads):
+    """The oracle's chunked prefill (kernel_prefill.cu:95-294 restated in numpy, fp32) on a
+    bounded sample of config 4: the first PREFILL_CPU_TOKENS tokens of its sequence 0, all
+    32 v-heads, from that sequence's initial state; single-threaded."""
+    from threadpoolctl import threadpool_limits
+    from oracle import gdn_oracle as O
+    p = workloads.config(4)
+    n = PREFILL_CPU_TOKENS
+    assert p["lengths"][0] >= n
+    f32 = lambda t: workloads.to_numpy(t).astype(np.float32)
+    args = [f32(p["q"][:n]), f32(p["k"][:n]), f32(p["v"][:n]), f32(p["state"][:1]), f32(p["A_log"]),
+            f32(p["a"][:n]), f32(p["dt_bias"]), f32(p["b"][:n])]
+    cu = np.array([0, n], np.int64)
+    times = []
+    with threadpool_limits(limits=1):
+        t_end = time.perf_counter() + seconds
+        while time.perf_counter() < t_end or len(times) < 3:
+            t0 = time.perf_counter()
+            O.prefill_chunked(*args, cu, p["scale"], dtype=np.float32)
+            times.append(time.perf_counter() - t0)
+    med = float(np.median(times))
+    return {"value": n / med, "unit": "tokens/s", "cores": 1, "kind": "port",
+            "us_per_sample": med * 1e6,
+            "sample": (f"oracle chunked prefill (numpy fp32, 1 thread) on the first {n} tokens "
+                       f"of config 4's sequence 0, 32 v-heads, its initial state; median of "
+                       f"{len(times)} runs over ~{seconds:.0f} s")}
+
+
 def load_traffic():
     """HBM bytes per decode launch measured with rocprofv3 PMC counters, if a
     measurement has been recorded under profiles/."""
@@ -300,6 +329,8 @@ def main():
             res["ms_per_step"] = round(res["prefill_varlen_32k"]["us"] / 1e3, 5)
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_baseline(args.cpu_seconds, workloads)
+        if args.only in ("prefill", "all"):
+            res["cpu_baseline_prefill"] = cpu_baseline_prefill(args.cpu_seconds / 2, workloads)
     print(json.dumps(res), flush=True)
 
 
