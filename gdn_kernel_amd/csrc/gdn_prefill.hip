@@ -1,7 +1,7 @@
 // GDN varlen chunked prefill for gfx950 (chunk C = 64, dk = dv = 128).
 //
-// One workgroup of 8 wavefronts walks the chunks of one (sequence, v-head)
-// chain as a two-stage pipeline:
+// A workgroup walks the chunks of one (sequence, v-head) chain, or of one slice
+// of its state rows, as a two-stage pipeline:
 //   * producer waves 4-7 prepare chunk t: stage K and Q in LDS, form the gates,
 //     the masked/decayed products N = strictLower(beta Gamma KK^T) and
 //     P = tril(Gamma QK^T), and T~ = (I + N)^-1;
@@ -10,9 +10,16 @@
 // chunk parity (V is single-buffered and rewritten only after it was read).
 // The roles hand chunks over through LDS counters, so each runs its own chain
 // and neither waits for the other's sub-steps.  The fp32 state never leaves the
-// register file: consumer wave w owns state rows v in [VW w, VW w + VW) (VW = 32
-// with the default four consumer waves) as MFMA accumulators (16x16 tiles of
-// S^T; lane = (k-group g = lane/16, column n = lane%16) holds S[v][k..k+3]).
+// register file: consumer wave w owns state rows v in [R0 + VW w, R0 + VW w + VW)
+// as MFMA accumulators (16x16 tiles of S^T; lane = (k-group g = lane/16,
+// column n = lane%16) holds S[v][k..k+3]).
+//
+// Launch variants (struct Variant): NCW consumer waves of VT 16-row tiles each
+// cover ROWS = 16 NCW VT state rows, so F = 128 / ROWS workgroups share a chain,
+// each owning rows [R0, R0 + ROWS).  They all prepare the same chunk data (the
+// producer work does not depend on the state) and each stages only its slice of
+// V.  Batches with many chains use F = 1 (four consumer waves of 32 rows); few
+// chains are split so that every CU gets a workgroup.
 //
 // Per chunk (positions >= clen are zero-padded: K = Q = V = 0, beta = 0 and
 // log-gate 0, as kernel_prefill.cu:102-114, 125-132 pads them):
@@ -45,6 +52,8 @@
 // leaving registers.  LDS tiles keep their contraction columns in that order
 // (perm32) so an operand row is one 16-byte read; an operand column of a
 // row-major tile is two ds_read_b64_tr_b16 (transpose reads within 16 lanes).
+#include <type_traits>
+
 #include "gdn_common.hpp"
 #include "gdn_launch.hpp"
 
@@ -62,18 +71,19 @@ constexpr int KSTR = 128;    // bf16 row stride of the K and Q tiles (16-byte sl
 constexpr int VSTR = 144;    // bf16 row stride of the V tile (rows 32 bytes apart modulo 128)
 constexpr int TSTR = 72;     // bf16 row stride of 64-wide tiles (T~, P, N)
 constexpr int NDB = 16 * 16 + 4;  // floats per diagonal N block (column-major; padded by 16 bytes)
-#ifndef GDN_PREFILL_CONSUMER_WAVES
-#define GDN_PREFILL_CONSUMER_WAVES 4
-#endif
-constexpr int NCW = GDN_PREFILL_CONSUMER_WAVES;  // consumer waves (4 or 8)
-constexpr int VT = 128 / (16 * NCW);             // 16-row state tiles per consumer wave
-constexpr int VW = 16 * VT;                      // state rows per consumer wave
-constexpr int NTHREADS = 64 * (NCW + 4);
-constexpr int NPROD = 256;   // producer threads (the last four waves)
-// The next chunk's K/Q loads go out at the start of the middle producer
-// sub-phase when registers allow (two waves per SIMD), else at the end of the tick.
-constexpr bool kEarlyPrefetch = NCW == 4;
 constexpr int NROWS = C - 16;  // rows of N kept for the off-diagonal solve
+
+template <int NCW_, int VT_>
+struct Variant {
+  static constexpr int NCW = NCW_;               // consumer waves
+  static constexpr int VT = VT_;                 // 16-row state tiles per consumer wave
+  static constexpr int VW = 16 * VT;             // state rows per consumer wave
+  static constexpr int ROWS = NCW * VW;          // state rows per workgroup
+  static constexpr int F = 128 / ROWS;           // workgroups per chain
+  static constexpr int NTHREADS = 64 * (NCW + 4);
+  static constexpr int VSEG = 8 * ROWS;          // 16-byte segments of the V slice of a chunk
+  static_assert(F * ROWS == 128 && NCW + 4 <= 8, "unsupported launch variant");
+};
 constexpr int kMaxSortedSeqs = 1024;  // longest-first ordering up to this many sequences
 
 struct __align__(16) PrefillSmem {
@@ -91,7 +101,7 @@ struct __align__(16) PrefillSmem {
   float eg[2][C];             // e^{gamma_c}
   float dd[2][C];             // e^{gamma_last - gamma_c}
   int seq;                    // sequence handled by this workgroup
-  int sync[8];                // hand-off counters (kReady, kVFree, kConsumed, kPPhase, kAbort, kDiagN)
+  int sync[8];                // hand-off counters (kReady, kVFree, kConsumed, kPPhase, kAbort, kDiagN, kX32)
 };
 
 constexpr float kLog2e = 1.4426950408889634f;
@@ -105,6 +115,19 @@ __device__ __forceinline__ f32x4 mfma(const uint4& a, const uint4& b, f32x4 c) {
 }
 
 __device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
+
+// Calls f(std::integral_constant<int, I>) for I = 0 .. N-1 (compile-time indices).
+template <int I, int N, class Fn>
+__device__ __forceinline__ void static_for_impl(Fn&& f) {
+  if constexpr (I < N) {
+    f(std::integral_constant<int, I>{});
+    static_for_impl<I + 1, N>(f);
+  }
+}
+template <int N, class Fn>
+__device__ __forceinline__ void static_for(Fn&& f) {
+  static_for_impl<0, N>(f);
+}
 
 // Position of contraction index r (0..31) inside a 32-wide permuted block.
 __device__ __forceinline__ int perm32(int r) { return ((r & 15) >> 2) * 8 + ((r >> 4) << 2) + (r & 3); }
@@ -159,6 +182,31 @@ __device__ __forceinline__ uint2 col4_tr_k(const uint16_t* tile, int k0, int col
 __device__ __forceinline__ uint4 frag_tr_k(const uint16_t* tile, int k0, int col0, int lane) {
   const uint2 a = col4_tr_k(tile, k0, col0, lane);
   const uint2 b = col4_tr_k(tile, k0 + 16, col0, lane);
+  return uint4{a.x, a.y, b.x, b.y};
+}
+
+// The same reads with the address split into lane bases and constants.  For
+// k0 a multiple of 16 and col0 = 16 kt, col4_tr_k reads element
+//   kq_off(k0 + rl, perm(16 kt + 4 (j & 3))),  rl = 4 g + j / 4,
+// and perm(16 kt + 4 (j & 3)) = 32 (kt / 2) + 8 (j & 3) + 4 (kt & 1), so with
+// s = sigma(rl) the offset is
+//   (k0 + rl) KSTR + 32 ((kt / 2) ^ (s >> 2)) + 8 ((j & 3) ^ (s & 3)) + 4 (kt & 1):
+// four lane bases (one per kt / 2) plus compile-time offsets.
+struct KtBases {
+  int b[4];
+};
+__device__ __forceinline__ KtBases kt_bases(int lane) {
+  const int j = lane & 15, rl = 4 * (lane >> 4) + (j >> 2), sl = kq_sigma(rl);
+  const int l0 = rl * KSTR + 8 * ((j & 3) ^ (sl & 3));
+  KtBases r;
+#pragma unroll
+  for (int m = 0; m < 4; ++m) r.b[m] = l0 + 32 * (m ^ (sl >> 2));
+  return r;
+}
+template <int KS, int KT>
+__device__ __forceinline__ uint4 frag_tr_k_at(const uint16_t* tile, const KtBases& kb) {
+  const uint16_t* p = tile + kb.b[KT / 2] + 32 * KS * KSTR + 4 * (KT & 1);
+  const uint2 a = read_tr(p), b = read_tr(p + 16 * KSTR);
   return uint4{a.x, a.y, b.x, b.y};
 }
 
@@ -238,7 +286,7 @@ __device__ __forceinline__ void wave_lds_sync() {
 // Hand-off between the two roles: monotonically increasing LDS counters.  A wave
 // signals by adding 1 after all its earlier LDS accesses completed (release); a
 // waiter polls until the count reaches its target (acquire).
-enum SyncCounter { kReady = 0, kVFree = 1, kConsumed = 2, kPPhase = 3, kAbort = 4, kDiagN = 5 };
+enum SyncCounter { kReady = 0, kVFree = 1, kConsumed = 2, kPPhase = 3, kAbort = 4, kDiagN = 5, kX32 = 6 };
 constexpr int kSpinLimit = 1 << 21;  // polls (about 70 ms) before a wait gives up
 
 __device__ __forceinline__ void signal_count(PrefillSmem& sm, int which, int lane) {
@@ -264,6 +312,47 @@ __device__ __forceinline__ void wait_count(PrefillSmem& sm, int which, int targe
   }
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 }
+
+#ifdef GDN_PREFILL_PHASE_CLOCKS
+// Development builds only (-DGDN_PREFILL_PHASE_CLOCKS): core-clock cycles that
+// each wave spends in each phase of its chunk loop, summed over its chunks, for
+// the first kClockWGs workgroups of a launch (read back with
+// gdn_prefill_phase_clocks_read).  Every lap is an s_memtime, whose wait also
+// drains the wave's outstanding LDS operations, so phases are slightly longer
+// than in the default build.
+}  // namespace
+constexpr int kClockPhases = 12, kClockWGs = 2048;
+__device__ uint32_t gdn_prefill_phase_clocks[kClockWGs * 8 * kClockPhases];
+namespace {
+struct PhaseClock {
+  uint64_t last;
+  uint32_t acc[kClockPhases];
+  __device__ __forceinline__ void start() {
+#pragma unroll
+    for (int i = 0; i < kClockPhases; ++i) acc[i] = 0;
+    last = __builtin_amdgcn_s_memtime();
+  }
+  __device__ __forceinline__ void lap(int ph) {
+    const uint64_t t = __builtin_amdgcn_s_memtime();
+    acc[ph] += uint32_t(t - last);
+    last = t;
+  }
+  __device__ __forceinline__ void store(int wave, int lane) {
+    if (blockIdx.x < unsigned(kClockWGs) && lane < kClockPhases) {
+      uint32_t v = 0;
+#pragma unroll
+      for (int i = 0; i < kClockPhases; ++i) v = lane == i ? acc[i] : v;
+      gdn_prefill_phase_clocks[(blockIdx.x * 8 + wave) * kClockPhases + lane] = v;
+    }
+  }
+};
+#else
+struct PhaseClock {
+  __device__ __forceinline__ void start() {}
+  __device__ __forceinline__ void lap(int) {}
+  __device__ __forceinline__ void store(int, int) {}
+};
+#endif
 
 // The parity-selected LDS buffers of one chunk.
 struct ChunkBufs {
@@ -400,7 +489,7 @@ __device__ __forceinline__ void diag_solve(PrefillSmem& sm, const ChunkBufs& cb,
   const int r = lane >> 4, j = lane & 15;
   const float* nb = sm.Nd + r * NDB;
   // Columns are read kColAhead steps ahead of their use.
-  constexpr int kColAhead = NCW == 4 ? 4 : 2;
+  constexpr int kColAhead = 4;
   f32x4 colv[15][4];
 #pragma unroll
   for (int m = 0; m < kColAhead; ++m)
@@ -500,223 +589,273 @@ __device__ __forceinline__ f32x4 finish_block(const ChunkBufs& cb, const f32x4& 
   return X;
 }
 
-// Off-diagonal blocks of T~ (one wavefront), as a 2x2 block inverse over the
-// 32x32 halves:  T~ = [[A^-1, 0], [-B^-1 C A^-1, B^-1]] with
+// Off-diagonal blocks of T~, as a 2x2 block inverse over the 32x32 halves:
+//   T~ = [[A^-1, 0], [-B^-1 C A^-1, B^-1]] with
 //   A^-1 = [[D0, 0], [X10, D1]],  B^-1 = [[D2, 0], [X32, D3]],  C = [[N20, N21], [N30, N31]],
 //   X10 = -D1 N10 D0,  X32 = -D3 N32 D2,  M = C A^-1,  [[X20, X21], [X30, X31]] = -B^-1 M.
-// The dependent chain is four products deep (N10 D0 -> X10 -> M20 / M30 -> X20 / X30).
-// X32 is also formed transposed (X32^T = G32^T (-D3)^T) so that its accumulator
-// serves as the A operand of X32 M.  Every LDS operand is read before the first
-// block store.
-__device__ __forceinline__ void solve_offdiagonal(const PrefillSmem& sm, const ChunkBufs& cb, int lane) {
-  const Pair2 d0 = diag_b(cb, 0, lane), d1 = diag_b(cb, 1, lane), d2 = diag_b(cb, 2, lane);
+// Two wavefronts share it.  Column 1 of M (N21 D1, N31 D1) does not need X10,
+// so one wave forms X32, X21 and X31 (offdiag_right) while the other forms X10,
+// X20 and X30 (offdiag_left); the left wave reads X32 back from T~ once the
+// right wave has stored it (counter kX32).  Each wave reads all of its LDS
+// operands before its first block store.
+__device__ __forceinline__ void offdiag_right(PrefillSmem& sm, const ChunkBufs& cb, int t, int lane) {
+  const Pair2 d1 = diag_b(cb, 1, lane), d2 = diag_b(cb, 2, lane);
+  const Pair2 a2 = block_a(cb.Th, cb.Tl, 0, 2, 2, lane), a3 = block_a(cb.Th, cb.Tl, 0, 3, 3, lane);
+  const Pair2 n21 = block_a(sm.Nh, sm.Nl, 16, 2, 1, lane), n31 = block_a(sm.Nh, sm.Nl, 16, 3, 1, lane),
+              n32 = block_a(sm.Nh, sm.Nl, 16, 3, 2, lane);
+  const f32x4 g32 = mul3_16(zero4(), n32, d2);
+  const f32x4 m21 = mul3_16(zero4(), n21, d1);
+  const f32x4 m31 = mul3_16(zero4(), n31, d1);
+  finish_block(cb, g32, a3, 3, 2, lane);  // X32
+  signal_count(sm, kX32, lane);
+  const Pair2 x32t = acc_b(mul3_16(zero4(), acc_b(-g32), a3));  // A operand holding X32
+  const Pair2 nm21 = acc_b(-m21), nm31 = acc_b(-m31);
+  store_block(cb, mul3_16(zero4(), a2, nm21), 2, 1, lane);                           // X21
+  store_block(cb, mul3_16(mul3_16(zero4(), x32t, nm21), a3, nm31), 3, 1, lane);      // X31
+  (void)t;
+}
+
+__device__ __forceinline__ void offdiag_left(PrefillSmem& sm, const ChunkBufs& cb, int t, int lane) {
+  const Pair2 d0 = diag_b(cb, 0, lane);
   const Pair2 a1 = block_a(cb.Th, cb.Tl, 0, 1, 1, lane), a2 = block_a(cb.Th, cb.Tl, 0, 2, 2, lane),
               a3 = block_a(cb.Th, cb.Tl, 0, 3, 3, lane);
   const Pair2 n10 = block_a(sm.Nh, sm.Nl, 16, 1, 0, lane), n20 = block_a(sm.Nh, sm.Nl, 16, 2, 0, lane),
               n21 = block_a(sm.Nh, sm.Nl, 16, 2, 1, lane), n30 = block_a(sm.Nh, sm.Nl, 16, 3, 0, lane),
-              n31 = block_a(sm.Nh, sm.Nl, 16, 3, 1, lane), n32 = block_a(sm.Nh, sm.Nl, 16, 3, 2, lane);
-  // products of diagonal blocks only
+              n31 = block_a(sm.Nh, sm.Nl, 16, 3, 1, lane);
   const f32x4 g10 = mul3_16(zero4(), n10, d0);
-  const f32x4 g32 = mul3_16(zero4(), n32, d2);
   const f32x4 p20 = mul3_16(zero4(), n20, d0);
   const f32x4 p30 = mul3_16(zero4(), n30, d0);
-  const f32x4 m21 = mul3_16(zero4(), n21, d1);
-  const f32x4 m31 = mul3_16(zero4(), n31, d1);
-  // X10, X32 (and X32^T)
-  const f32x4 x10 = finish_block(cb, g10, a1, 1, 0, lane);
-  finish_block(cb, g32, a3, 3, 2, lane);
-  const Pair2 x32t = acc_b(mul3_16(zero4(), acc_b(-g32), a3));  // A operand holding X32
-  // M = C A^-1 (column 0 needs X10; column 1 is N21 D1, N31 D1)
+  const f32x4 x10 = finish_block(cb, g10, a1, 1, 0, lane);  // X10
   const Pair2 b10 = acc_b(x10);
   const Pair2 nm20 = acc_b(-mul3_16(p20, n21, b10));
   const Pair2 nm30 = acc_b(-mul3_16(p30, n31, b10));
-  const Pair2 nm21 = acc_b(-m21), nm31 = acc_b(-m31);
-  // -B^-1 M
-  store_block(cb, mul3_16(zero4(), a2, nm20), 2, 0, lane);
-  store_block(cb, mul3_16(zero4(), a2, nm21), 2, 1, lane);
-  store_block(cb, mul3_16(mul3_16(zero4(), x32t, nm20), a3, nm30), 3, 0, lane);
-  store_block(cb, mul3_16(mul3_16(zero4(), x32t, nm21), a3, nm31), 3, 1, lane);
+  store_block(cb, mul3_16(zero4(), a2, nm20), 2, 0, lane);  // X20
+  const f32x4 x30 = mul3_16(zero4(), a3, nm30);
+  wait_count(sm, kX32, t + 1);  // X32 stored by the right wave
+  const Pair2 x32 = block_a(cb.Th, cb.Tl, 0, 3, 2, lane);
+  store_block(cb, mul3_16(x30, x32, nm20), 3, 0, lane);     // X30
 }
+
+// Global loads.  A CU streams about 48 KB of K, Q and V per chunk through its
+// vector-memory pipe, and a wave that issues loads while that queue is full
+// stalls until it drains.  The producers issue the next chunk's K/Q loads at
+// the start of their middle step, while the consumers' retrieve (the heaviest
+// LDS reader) runs, so the stall overlaps LDS work that would hold them up
+// anyway.
+//
+// Producer thread pt (0..255) owns K/Q segments pt + 256 it (it = 0..3): token
+// pt/16 + 16 it, columns 8 (pt%16) .. +7 (16 consecutive threads read one
+// 256-byte row).  Addresses are a wave-uniform chunk base (64-bit, scalar) plus
+// a 32-bit lane offset that is fixed across chunks.
+constexpr int NPROD = 256;  // producer threads (four waves)
 
 struct ProducerPrefetch {
   uint4 k[4], q[4];
   uint16_t a, b;  // raw gate inputs of token pt (first producer wave only)
 };
 
-// Producer thread pt's K/Q segments of a chunk: segment pt + 256*it is token
-// seg/16, columns 8*(seg%16) .. +7 (16 consecutive threads read one 256-byte row).
+struct LaneOffsets {
+  int k, q;  // (pt/16) rows + 8 (pt%16) elements, in the K and Q row strides
+  int ab;    // pt rows of the a/b [T, Hv] layout
+};
+
 __device__ __forceinline__ void producer_prefetch(const PrefillArgs& p, int64_t cs, int clen, int h, int hq, int hk,
-                                                  int pt, ProducerPrefetch& f) {
+                                                  int pt, const LaneOffsets& lo, ProducerPrefetch& f) {
+  const uint16_t* kb = p.k + (cs * p.Hk + hk) * D;
+  const uint16_t* qb = p.q + (cs * p.Hq + hq) * D;
 #pragma unroll
   for (int it = 0; it < 4; ++it) {
-    const int seg = pt + it * NPROD, c = seg >> 4, sg = seg & 15;
+    const int c = (pt >> 4) + 16 * it;
     f.k[it] = f.q[it] = uint4{0u, 0u, 0u, 0u};
     if (c < clen) {
-      f.k[it] = *reinterpret_cast<const uint4*>(p.k + ((cs + c) * p.Hk + hk) * D + 8 * sg);
-      f.q[it] = *reinterpret_cast<const uint4*>(p.q + ((cs + c) * p.Hq + hq) * D + 8 * sg);
+      f.k[it] = *reinterpret_cast<const uint4*>(kb + (lo.k + 16 * it * p.Hk * D));
+      f.q[it] = *reinterpret_cast<const uint4*>(qb + (lo.q + 16 * it * p.Hq * D));
     }
   }
   if (pt < 64) {  // wave-uniform; the row index is clamped and padding masked when used
-    const int64_t idx = (cs + (pt < clen ? pt : clen - 1)) * p.Hv + h;
-    f.a = p.a[idx];
-    f.b = p.b[idx];
+    const int off = pt < clen ? lo.ab : (clen - 1) * p.Hv;
+    f.a = (p.a + cs * p.Hv + h)[off];
+    f.b = (p.b + cs * p.Hv + h)[off];
   }
 }
 
 // The producer loop: chunk t is prepared into the buffers of parity t & 1 once
 // the consumers are done with chunk t - 2 (same parity).  The four producer waves
 // meet twice per chunk (after staging; after the tiles and diagonal blocks) on
-// their own counter; the chunk is handed over when all four are done.
+// their own counter; the chunk is handed over when all four are done.  V is
+// staged for the workgroup's state rows [row0, row0 + ROWS) only.
+template <class V>
 __device__ __forceinline__ void producer_loop(PrefillSmem& sm, const PrefillArgs& p, int64_t s0, int64_t s1,
-                                              int nchunks, int h, int hq, int hk, int pw, int lane0) {
+                                              int nchunks, int h, int hq, int hk, int row0, int pw, int lane0) {
+  constexpr int NVIT = (V::VSEG + NPROD - 1) / NPROD;  // V segments per producer thread
   const int pt = pw * 64 + lane0;
   const float neg_decay = -expf(p.A_log[h]);
   const float dt_bias = p.dt_bias[h];
+  const LaneOffsets lo = {(pt >> 4) * p.Hk * D + 8 * (pt & 15), (pt >> 4) * p.Hq * D + 8 * (pt & 15), pt * p.Hv};
+  // V slice: segment pt + 256 it is token c, columns row0 + 8 sg .. +7.
+  int voff[NVIT], vrow[NVIT];
+#pragma unroll
+  for (int it = 0; it < NVIT; ++it) {
+    const int seg = pt + it * NPROD, c = seg / (V::ROWS / 8), sg = seg % (V::ROWS / 8);
+    vrow[it] = seg < V::VSEG ? c : C;  // C: no segment
+    voff[it] = c * p.Hv * D + 8 * sg;
+  }
   ProducerPrefetch f;
-  uint4 fv[4];
-  producer_prefetch(p, s0, int(s1 - s0 < C ? s1 - s0 : C), h, hq, hk, pt, f);
+  uint4 fv[NVIT];
+  producer_prefetch(p, s0, int(s1 - s0 < C ? s1 - s0 : C), h, hq, hk, pt, lo, f);
+  PhaseClock clk;
+  clk.start();
 
   for (int t = 0; t < nchunks; ++t) {
     // The lane index is re-materialised opaquely each tick so that lane-dependent
     // LDS addresses are recomputed in the loop rather than hoisted and spilled.
     int lane = lane0;
     asm volatile("" : "+v"(lane));
-    constexpr bool work = true;
     const int64_t cs = s0 + int64_t(t) * C;
     const int clen = int(s1 - cs < C ? s1 - cs : C);
+    const int64_t ncs = cs + C;
+    const int nclen = int(s1 - ncs < C ? s1 - ncs : C);
     const ChunkBufs cb = chunk_bufs(sm, t & 1);
-    if (t >= 2) wait_count(sm, kConsumed, 4 * (t - 1));  // chunk t - 2 consumed
+    if (t >= 2) wait_count(sm, kConsumed, V::NCW * (t - 1));  // chunk t - 2 consumed
+    clk.lap(0);
 
     // 1: stage K/Q (permuted columns), gates
-    if (work) {
 #pragma unroll
-      for (int it = 0; it < 4; ++it) {
-        const int seg = pt + it * NPROD, c = seg >> 4, sg = seg & 15;
-        const int col0 = (8 * sg) & ~31, r0 = (8 * sg) & 31;
-        const int pa = kq_off(c, col0 + perm32(r0)), pb = kq_off(c, col0 + perm32(r0 + 4));
-        *reinterpret_cast<uint2*>(cb.K + pa) = uint2{f.k[it].x, f.k[it].y};
-        *reinterpret_cast<uint2*>(cb.K + pb) = uint2{f.k[it].z, f.k[it].w};
-        *reinterpret_cast<uint2*>(cb.Q + pa) = uint2{f.q[it].x, f.q[it].y};
-        *reinterpret_cast<uint2*>(cb.Q + pb) = uint2{f.q[it].z, f.q[it].w};
-      }
-      if (pw == 0) {
-        const float lg = lane < clen ? fast_log_gate(neg_decay, bf16_to_f32(f.a) + dt_bias) : 0.f;
-        const float bt = lane < clen ? fast_sigmoid(bf16_to_f32(f.b)) : 0.f;
-        const float gm = wave_inclusive_scan(lg);
-        const float glast = readlane_f(gm, clen - 1);
-        cb.gam[lane] = gm;
-        cb.bet[lane] = bt;
-        cb.eg[lane] = exp_le0(gm);
-        cb.dd[lane] = exp_le0(glast - gm);
-      }
-      // V of this chunk into registers; staged at the end of the tick, after the
-      // consumers' last read of the previous chunk's V.
+    for (int it = 0; it < 4; ++it) {
+      const int c = (pt >> 4) + 16 * it, sg = pt & 15;
+      const int col0 = (8 * sg) & ~31, r0 = (8 * sg) & 31;
+      const int pa = kq_off(c, col0 + perm32(r0)), pb = kq_off(c, col0 + perm32(r0 + 4));
+      *reinterpret_cast<uint2*>(cb.K + pa) = uint2{f.k[it].x, f.k[it].y};
+      *reinterpret_cast<uint2*>(cb.K + pb) = uint2{f.k[it].z, f.k[it].w};
+      *reinterpret_cast<uint2*>(cb.Q + pa) = uint2{f.q[it].x, f.q[it].y};
+      *reinterpret_cast<uint2*>(cb.Q + pb) = uint2{f.q[it].z, f.q[it].w};
+    }
+    if (pw == 0) {
+      const float lg = lane < clen ? fast_log_gate(neg_decay, bf16_to_f32(f.a) + dt_bias) : 0.f;
+      const float bt = lane < clen ? fast_sigmoid(bf16_to_f32(f.b)) : 0.f;
+      const float gm = wave_inclusive_scan(lg);
+      const float glast = readlane_f(gm, clen - 1);
+      cb.gam[lane] = gm;
+      cb.bet[lane] = bt;
+      cb.eg[lane] = exp_le0(gm);
+      cb.dd[lane] = exp_le0(glast - gm);
+    }
+    // The V slice of this chunk into registers; staged at the end of the tick,
+    // after the consumers' last read of the previous chunk's V.
+    {
+      const uint16_t* vb = p.v + (cs * p.Hv + h) * D + row0;
 #pragma unroll
-      for (int it = 0; it < 4; ++it) {
-        const int seg = pt + it * NPROD, c = seg >> 4, sg = seg & 15;
+      for (int it = 0; it < NVIT; ++it) {
         fv[it] = uint4{0u, 0u, 0u, 0u};
-        if (c < clen) fv[it] = *reinterpret_cast<const uint4*>(p.v + ((cs + c) * p.Hv + h) * D + 8 * sg);
+        if (vrow[it] < clen) fv[it] = *reinterpret_cast<const uint4*>(vb + voff[it]);
       }
     }
+    clk.lap(1);
     signal_count(sm, kPPhase, lane);
     wait_count(sm, kPPhase, 4 * (2 * t + 1));  // all of K/Q/gates staged
+    clk.lap(2);
     // The rest of the chunk is the longer chain: producer waves go ahead of the
     // consumer wave sharing the SIMD.
     __builtin_amdgcn_s_setprio(1);
 
-    // 2: next chunk's K/Q/a/b into registers (staged at the next chunk's start);
-    // diagonal blocks of T~ (first producer wave), N tiles (the others)
-    if (work) {
-      if (kEarlyPrefetch) {
-        const int64_t ncs = cs + C;
-        if (ncs < s1) producer_prefetch(p, ncs, int(s1 - ncs < C ? s1 - ncs : C), h, hq, hk, pt, f);
+    // 2: the next chunk's K/Q loads; diagonal N tiles (the solve waits for
+    // them); then the diagonal blocks of T~ (wave 0) or the off-diagonal N tiles
+    // and one P tile each (the others).
+    if (ncs < s1) producer_prefetch(p, ncs, nclen, h, hq, hk, pt, lo, f);
+    clk.lap(10);
+    switch (pw) {
+      case 0:
+        diag_tiles<0, 1>(sm, cb, lane);
+        signal_count(sm, kDiagN, lane);
+        clk.lap(3);
+        wait_count(sm, kDiagN, 4 * (t + 1));
+        clk.lap(4);
+        diag_solve(sm, cb, lane);
+        clk.lap(5);
+        break;
+      case 1: {
+        diag_tiles<1, 2>(sm, cb, lane);
+        signal_count(sm, kDiagN, lane);
+        const TileJob j1[2] = {{1, 1, 0}, {1, 2, 0}};
+        run_tiles(sm, cb, j1, p.scale, lane);
+        const TileJob j2[1] = {{2, 0, 0}};
+        run_tiles(sm, cb, j2, p.scale, lane);
+        break;
       }
-      // The diagonal N tiles come first (the solve waits for them), then the
-      // off-diagonal N tiles; the P tiles wait for the last sub-phase.
-      switch (pw) {
-        case 0:
-          diag_tiles<0, 1>(sm, cb, lane);
-          signal_count(sm, kDiagN, lane);
-          wait_count(sm, kDiagN, 4 * (t + 1));
-          diag_solve(sm, cb, lane);
-          break;
-        case 1: {
-          diag_tiles<1, 2>(sm, cb, lane);
-          signal_count(sm, kDiagN, lane);
-          const TileJob j1[2] = {{1, 1, 0}, {1, 2, 0}};
-          run_tiles(sm, cb, j1, p.scale, lane);
-          break;
-        }
-        case 2: {
-          diag_tiles<2, 3>(sm, cb, lane);
-          signal_count(sm, kDiagN, lane);
-          const TileJob j1[2] = {{1, 3, 0}, {1, 2, 1}};
-          run_tiles(sm, cb, j1, p.scale, lane);
-          break;
-        }
-        default: {
-          diag_tiles<3, 4>(sm, cb, lane);
-          signal_count(sm, kDiagN, lane);
-          const TileJob j1[2] = {{1, 3, 1}, {1, 3, 2}};
-          run_tiles(sm, cb, j1, p.scale, lane);
-          break;
-        }
+      case 2: {
+        diag_tiles<2, 3>(sm, cb, lane);
+        signal_count(sm, kDiagN, lane);
+        const TileJob j1[2] = {{1, 3, 0}, {1, 2, 1}};
+        run_tiles(sm, cb, j1, p.scale, lane);
+        const TileJob j2[1] = {{2, 1, 0}};
+        run_tiles(sm, cb, j2, p.scale, lane);
+        break;
+      }
+      default: {
+        diag_tiles<3, 4>(sm, cb, lane);
+        signal_count(sm, kDiagN, lane);
+        const TileJob j1[2] = {{1, 3, 1}, {1, 3, 2}};
+        run_tiles(sm, cb, j1, p.scale, lane);
+        const TileJob j2[1] = {{2, 1, 1}};
+        run_tiles(sm, cb, j2, p.scale, lane);
+        break;
       }
     }
+    clk.lap(3);
     signal_count(sm, kPPhase, lane);
     wait_count(sm, kPPhase, 4 * (2 * t + 2));  // diagonal blocks and N tiles done
+    clk.lap(6);
 
-    // 3: off-diagonal blocks of T~ (last producer wave), P tiles (the others), V
-    // once the consumers have read the previous chunk's
-    if (work) {
-      switch (pw) {
-        case 0: {
-          const TileJob j1[2] = {{2, 0, 0}, {2, 1, 0}};
-          run_tiles(sm, cb, j1, p.scale, lane);
-          const TileJob j2[2] = {{2, 1, 1}, {2, 2, 0}};
-          run_tiles(sm, cb, j2, p.scale, lane);
-          break;
-        }
-        case 1: {
-          const TileJob j1[2] = {{2, 2, 1}, {2, 2, 2}};
-          run_tiles(sm, cb, j1, p.scale, lane);
-          const TileJob j2[1] = {{2, 3, 0}};
-          run_tiles(sm, cb, j2, p.scale, lane);
-          break;
-        }
-        case 2: {
-          const TileJob j1[2] = {{2, 3, 1}, {2, 3, 2}};
-          run_tiles(sm, cb, j1, p.scale, lane);
-          const TileJob j2[1] = {{2, 3, 3}};
-          run_tiles(sm, cb, j2, p.scale, lane);
-          break;
-        }
-        default:
-          solve_offdiagonal(sm, cb, lane);
-          break;
+    // 3: off-diagonal blocks of T~ (waves 1 and 3), the remaining P tiles (waves
+    // 0 and 2, one on wave 1), V once the consumers have read the previous chunk's
+    switch (pw) {
+      case 0: {
+        const TileJob j1[2] = {{2, 2, 0}, {2, 2, 1}};
+        run_tiles(sm, cb, j1, p.scale, lane);
+        const TileJob j2[1] = {{2, 2, 2}};
+        run_tiles(sm, cb, j2, p.scale, lane);
+        break;
       }
-      if (t >= 1) wait_count(sm, kVFree, 4 * t);
+      case 1: {
+        offdiag_right(sm, cb, t, lane);
+        const TileJob j1[1] = {{2, 3, 3}};
+        run_tiles(sm, cb, j1, p.scale, lane);
+        break;
+      }
+      case 2: {
+        const TileJob j1[2] = {{2, 3, 0}, {2, 3, 1}};
+        run_tiles(sm, cb, j1, p.scale, lane);
+        const TileJob j2[1] = {{2, 3, 2}};
+        run_tiles(sm, cb, j2, p.scale, lane);
+        break;
+      }
+      default:
+        offdiag_left(sm, cb, t, lane);
+        break;
+    }
+    clk.lap(7);
+    if (t >= 1) wait_count(sm, kVFree, V::NCW * t);
+    clk.lap(8);
 #pragma unroll
-      for (int it = 0; it < 4; ++it) {
-        const int seg = pt + it * NPROD;
-        *reinterpret_cast<uint4*>(sm.V + (seg >> 4) * VSTR + 8 * (seg & 15)) = fv[it];
-      }
-      if (!kEarlyPrefetch) {
-        const int64_t ncs = cs + C;
-        if (ncs < s1) producer_prefetch(p, ncs, int(s1 - ncs < C ? s1 - ncs : C), h, hq, hk, pt, f);
-      }
+    for (int it = 0; it < NVIT; ++it) {
+      const int seg = pt + it * NPROD;
+      if (seg < V::VSEG)
+        *reinterpret_cast<uint4*>(sm.V + (seg / (V::ROWS / 8)) * VSTR + 8 * (seg % (V::ROWS / 8))) = fv[it];
     }
     __builtin_amdgcn_s_setprio(0);
     signal_count(sm, kReady, lane);
+    clk.lap(9);
   }
+  clk.store(V::NCW + pw, lane0);
 }
 
 // ---------------------------------------------------------------------------
-// Consumer side (waves 0-3; wave w owns state rows 32w .. 32w+31)
+// Consumer side (waves 0 .. NCW-1; wave w owns state rows R0 + VW w .. + VW - 1)
 // ---------------------------------------------------------------------------
 
 // Xk = K S^T (rows c, cols v) with S as hi/lo B operands, and Xq = (Q S^T)^T
 // (rows v, cols c) with S's hi part as the A operand (output-only product).
+template <int VT>
 __device__ __forceinline__ void retrieve(const ChunkBufs& cb, const f32x4 (&S)[VT][8], f32x4 (&Xk)[4][VT],
                                          f32x4 (&Xq)[VT][4], int lane) {
 #pragma unroll
@@ -744,12 +883,21 @@ __device__ __forceinline__ void retrieve(const ChunkBufs& cb, const f32x4 (&S)[V
 
 // The consumer loop: iteration t (>= 1) advances the state through chunk t-1
 // from the buffers of parity (t-1) & 1, once the producers have handed it over.
+// The wave's rows are row0 + VW wave + 16 vt + lane%16 (V columns VW wave + ...
+// of the staged slice).
+template <class V>
 __device__ __forceinline__ void consumer_loop(PrefillSmem& sm, const PrefillArgs& p, int64_t s0, int64_t s1,
-                                              int nchunks, int h, int wave, int lane0, f32x4 (&S)[VT][8]) {
+                                              int nchunks, int h, int row0, int wave, int lane0,
+                                              f32x4 (&S)[V::VT][8]) {
+  constexpr int VT = V::VT, VW = V::VW;
   const int64_t vstride = int64_t(p.Hv) * D;
-  int orow[4];  // element offset of output row 16ct + lane%16 from the chunk start
+  // Element offset of output row 16ct + lane%16, columns 4 (lane/16) .. +3, from
+  // the wave's (uniform) chunk base.
+  int orow[4];
 #pragma unroll
-  for (int ct = 0; ct < 4; ++ct) orow[ct] = (16 * ct + (lane0 & 15)) * int(vstride);
+  for (int ct = 0; ct < 4; ++ct) orow[ct] = (16 * ct + (lane0 & 15)) * int(vstride) + 4 * (lane0 >> 4);
+  PhaseClock clk;
+  clk.start();
   for (int t = 1; t <= nchunks; ++t) {
     int lane = lane0;
     asm volatile("" : "+v"(lane));
@@ -758,10 +906,12 @@ __device__ __forceinline__ void consumer_loop(PrefillSmem& sm, const PrefillArgs
     const int clen = int(s1 - cs < C ? s1 - cs : C);
     const ChunkBufs cb = chunk_bufs(sm, (t - 1) & 1);
     wait_count(sm, kReady, 4 * t);  // chunk t - 1 prepared
+    clk.lap(0);
 
     // 1: X = K S^T, (Q S^T)^T
     f32x4 Xk[4][VT], Xq[VT][4];
     retrieve(cb, S, Xk, Xq, lane);
+    clk.lap(1);
 
     // 2: Y, v_new, output
     // Y = beta (V - e^gamma X); element (c = 16ct + 4g + i, v = VW w + 16vt + n16).
@@ -783,6 +933,7 @@ __device__ __forceinline__ void consumer_loop(PrefillSmem& sm, const PrefillArgs
       for (int vt = 0; vt < VT; ++vt) Xq[vt][ct] = Xq[vt][ct] * ecn;
     }
     signal_count(sm, kVFree, lane);  // V of this chunk read
+    clk.lap(2);
     // v_new = T~ Y (contraction over the rows of Y in blocks js; T~ is lower triangular).
     uint4 Yh[VT][2], Yl[VT][2];
 #pragma unroll
@@ -806,6 +957,7 @@ __device__ __forceinline__ void consumer_loop(PrefillSmem& sm, const PrefillArgs
         }
       }
     }
+    clk.lap(3);
     // o^T = scale e^gamma (S Q^T) + v_new^T (scale P)^T (rows v, cols c); P is lower triangular.
 #pragma unroll
     for (int js = 0; js < 2; ++js) {
@@ -819,8 +971,8 @@ __device__ __forceinline__ void consumer_loop(PrefillSmem& sm, const PrefillArgs
         for (int vt = 0; vt < VT; ++vt) Xq[vt][ct] = mfma(vb[vt], pq, Xq[vt][ct]);
       }
     }
-    // Lane holds o[c = 16ct + n16][v = VW w + 16vt + 4g .. +3]: one 8-byte store each.
-    uint16_t* obase = p.out + cs * vstride + (int64_t(h) * D + VW * wave + 4 * g);
+    // Lane holds o[c = 16ct + n16][v = row0 + VW w + 16vt + 4g .. +3]: one 8-byte store each.
+    uint16_t* obase = p.out + cs * vstride + (int64_t(h) * D + row0 + VW * wave);
 #pragma unroll
     for (int ct = 0; ct < 4; ++ct) {
       if (16 * ct + n16 < clen) {
@@ -832,6 +984,7 @@ __device__ __forceinline__ void consumer_loop(PrefillSmem& sm, const PrefillArgs
       }
     }
 
+    clk.lap(4);
     // 3: S = e^{gamma_last} S + sum_c K[c]^T (d_c v_new[c]),  d_c = e^{gamma_last - gamma_c}
     const float dlast = cb.eg[clen - 1];
     uint4 Uh[VT][2], Ul[VT][2];
@@ -843,26 +996,30 @@ __device__ __forceinline__ void consumer_loop(PrefillSmem& sm, const PrefillArgs
 #pragma unroll
       for (int vt = 0; vt < VT; ++vt) split_pack(Vn[2 * js][vt] * e0, Vn[2 * js + 1][vt] * e1, Uh[vt][js], Ul[vt][js]);
     }
-#pragma unroll
-    for (int kt = 0; kt < 8; ++kt) {
+    const KtBases kb = kt_bases(lane);
+    static_for<8>([&](auto KT) {
+      constexpr int kt = decltype(KT)::value;
 #pragma unroll
       for (int vt = 0; vt < VT; ++vt) S[vt][kt] = S[vt][kt] * dlast;
-#pragma unroll
-      for (int js = 0; js < 2; ++js) {
-        const uint4 ak = frag_tr_k(cb.K, 32 * js, 16 * kt, lane);
+      static_for<2>([&](auto JS) {
+        constexpr int js = decltype(JS)::value;
+        const uint4 ak = frag_tr_k_at<js, kt>(cb.K, kb);
 #pragma unroll
         for (int vt = 0; vt < VT; ++vt) {
           S[vt][kt] = mfma(ak, Uh[vt][js], S[vt][kt]);
           S[vt][kt] = mfma(ak, Ul[vt][js], S[vt][kt]);
         }
-      }
-    }
+      });
+    });
     signal_count(sm, kConsumed, lane);  // buffers of this chunk no longer read
+    clk.lap(5);
   }
+  clk.store(wave, lane0);
 }
 
 // The sequence of rank `rank` in descending length order (ties: lower index
 // first), so the longest chains start first; natural order for large batches.
+template <int NTHREADS>
 __device__ int pick_sequence(PrefillSmem& sm, const PrefillArgs& p, int rank, int tid) {
   if (p.N <= 1 || p.N > kMaxSortedSeqs) return rank;
   int* len = reinterpret_cast<int*>(sm.Nh);  // scratch until the first chunk
@@ -886,15 +1043,25 @@ __device__ int pick_sequence(PrefillSmem& sm, const PrefillArgs& p, int rank, in
   return sm.seq;
 }
 
-__global__ __launch_bounds__(NTHREADS) void gdn_prefill_kernel(PrefillArgs p) {
+// Workgroup b handles slice f of chain `chain` (chain = rank-major, v-head
+// minor).  With F > 1 the F slices of a chain are b = 8 F (chain / 8) + 8 f +
+// chain % 8: workgroups are dealt to the XCDs round-robin, so the slices of one
+// chain share an XCD (and its L2) for their common K/Q/V reads.
+template <class V>
+__global__ __launch_bounds__(V::NTHREADS) void gdn_prefill_kernel(PrefillArgs p) {
+  constexpr int NCW = V::NCW, VT = V::VT, VW = V::VW, NTHREADS = V::NTHREADS;
   __shared__ PrefillSmem sm;
 
   const int tid = threadIdx.x;
   const int lane0 = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
 
-  const int h = blockIdx.x % p.Hv;
-  const int seq = pick_sequence(sm, p, blockIdx.x / p.Hv, tid);
+  const int bid = blockIdx.x;
+  const int chain = V::F == 1 ? bid : (bid / (8 * V::F)) * 8 + bid % 8;
+  const int row0 = V::F == 1 ? 0 : ((bid / 8) % V::F) * V::ROWS;
+  if (chain >= p.N * p.Hv) return;  // padding of the last group of eight chains (workgroup-uniform)
+  const int h = chain % p.Hv;
+  const int seq = pick_sequence<NTHREADS>(sm, p, chain / p.Hv, tid);
   const int hq = h / (p.Hv / p.Hq);
   const int hk = h / (p.Hv / p.Hk);
 
@@ -926,17 +1093,17 @@ __global__ __launch_bounds__(NTHREADS) void gdn_prefill_kernel(PrefillArgs p) {
   __syncthreads();  // cleared LDS and counters visible to both roles
 
   if (wave >= NCW) {
-    if (nchunks > 0) producer_loop(sm, p, s0, s1, nchunks, h, hq, hk, wave - NCW, lane0);
+    if (nchunks > 0) producer_loop<V>(sm, p, s0, s1, nchunks, h, hq, hk, row0, wave - NCW, lane0);
     return;
   }
 
-  // Consumer state slab: rows v = VW*wave + 16*vt + n16, cols k = 16*kt + 4g + i.
+  // Consumer state slab: rows v = row0 + VW*wave + 16*vt + n16, cols k = 16*kt + 4g + i.
   const int64_t state_head = (int64_t(seq) * p.Hv + h) * D * D;
   const int g = lane0 >> 4, n16 = lane0 & 15;
   f32x4 S[VT][8];
 #pragma unroll
   for (int vt = 0; vt < VT; ++vt) {
-    const int v = VW * wave + 16 * vt + n16;
+    const int v = row0 + VW * wave + 16 * vt + n16;
 #pragma unroll
     for (int kt = 0; kt < 8; ++kt) {
       if (p.state) {
@@ -947,13 +1114,13 @@ __global__ __launch_bounds__(NTHREADS) void gdn_prefill_kernel(PrefillArgs p) {
       }
     }
   }
-  if (nchunks > 0) consumer_loop(sm, p, s0, s1, nchunks, h, wave, lane0, S);
+  if (nchunks > 0) consumer_loop<V>(sm, p, s0, s1, nchunks, h, row0, wave, lane0, S);
 
   // Final state (for an empty sequence: the initial state, or zeros).
   if (nchunks > 0 || p.state != p.new_state) {
 #pragma unroll
     for (int vt = 0; vt < VT; ++vt) {
-      const int v = VW * wave + 16 * vt + n16;
+      const int v = row0 + VW * wave + 16 * vt + n16;
 #pragma unroll
       for (int kt = 0; kt < 8; ++kt) {
         const f32x4 x = S[vt][kt];
@@ -964,12 +1131,56 @@ __global__ __launch_bounds__(NTHREADS) void gdn_prefill_kernel(PrefillArgs p) {
   }
 }
 
-}  // namespace
-
-hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream) {
-  const int64_t grid = int64_t(a.N) * a.Hv;
-  hipLaunchKernelGGL(gdn_prefill_kernel, dim3(unsigned(grid)), dim3(NTHREADS), 0, stream, a);
+template <class V>
+hipError_t launch_variant(const PrefillArgs& a, hipStream_t stream) {
+  const int64_t chains = int64_t(a.N) * a.Hv;
+  const int64_t grid = V::F == 1 ? chains : (chains + 7) / 8 * 8 * V::F;
+  hipLaunchKernelGGL(gdn_prefill_kernel<V>, dim3(unsigned(grid)), dim3(V::NTHREADS), 0, stream, a);
   return hipGetLastError();
 }
 
+// Compute units of the current device (queried once per device).
+int device_cus() {
+  static int cus[64] = {0};
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
+  if (cus[dev] == 0) {
+    int n = 0;
+    if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
+    cus[dev] = n;
+  }
+  return cus[dev];
+}
+
+}  // namespace
+
+#ifndef GDN_PREFILL_MAX_SPLIT
+#define GDN_PREFILL_MAX_SPLIT 8
+#endif
+
+// Chains are split F ways (F a power of two, at most GDN_PREFILL_MAX_SPLIT)
+// while the split grid still fits one workgroup per CU.
+hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream) {
+  const int64_t chains = int64_t(a.N) * a.Hv;
+  const int64_t cus = device_cus();
+  int F = 1;
+  while (F < GDN_PREFILL_MAX_SPLIT && chains * 2 * F <= cus) F *= 2;
+  switch (F) {
+    case 1: return launch_variant<Variant<4, 2>>(a, stream);
+    case 2: return launch_variant<Variant<2, 2>>(a, stream);
+    case 4: return launch_variant<Variant<1, 2>>(a, stream);
+    default: return launch_variant<Variant<1, 1>>(a, stream);
+  }
+}
+
 }  // namespace gdn
+
+#ifdef GDN_PREFILL_PHASE_CLOCKS
+// Copies the phase clocks of the last launch ([kClockWGs][8][kClockPhases]
+// uint32) to host memory; development builds only.
+extern "C" int gdn_prefill_phase_clocks_read(uint32_t* host, int64_t count) {
+  const int64_t n = count < int64_t(gdn::kClockWGs) * 8 * gdn::kClockPhases
+                        ? count : int64_t(gdn::kClockWGs) * 8 * gdn::kClockPhases;
+  return hipMemcpyFromSymbol(host, HIP_SYMBOL(gdn::gdn_prefill_phase_clocks), size_t(n) * 4) == hipSuccess ? 0 : 3;
+}
+#endif

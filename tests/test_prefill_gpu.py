@@ -177,3 +177,33 @@ def test_prefill_config4_full_size(gpu):
         o1, s1 = run_prefill(sub, gpu)
         torch.cuda.synchronize()
         assert torch.equal(o1, out[s:e]) and torch.equal(s1[0], ns[i]), f"seq {i} packed != alone"
+
+
+def test_prefill_split_variants_bitwise(gpu):
+    """Chains are split over 8, 4, 2 or 1 workgroups depending on how many (sequence,
+    v-head) chains the batch has.  Every split does the same per-row arithmetic, so
+    padding a batch with empty sequences (more chains, a smaller split) must not change
+    a single bit of the real sequences' outputs and states; the smallest batch is also
+    checked against the oracle."""
+    heads = Heads(4, 4, 8)
+    real = [150, 64, 7]
+    p = workloads.prefill_inputs(real + [0] * 17, heads, seed=16, gate="slow", state_scale=0.5)
+    results = []
+    for n in (3, 5, 13, 20):          # 24, 40, 104, 160 chains: splits 8, 4, 2, 1 on 256 CUs
+        say(f"prefill split variants: {n} sequences ({n * heads.hv} chains)")
+        sub = dict(p)
+        sub["cu_seqlens"] = p["cu_seqlens"][:n + 1]
+        sub["state"] = p["state"][:n]
+        out, ns = run_prefill(sub, gpu)
+        torch.cuda.synchronize()
+        results.append((out, ns[:len(real)]))
+        if n == 3:
+            o_ref, s_ref = oracle_prefill(sub)
+            assert_close(host(out), o_ref, OUT_RTOL, OUT_ATOL, "output")
+            assert_close(host(ns), s_ref, STATE_RTOL, STATE_ATOL, "new_state")
+        else:
+            assert not host(ns[len(real):] - sub["state"][len(real):].to(gpu)).any(), \
+                "empty sequences must pass their state through"
+    for i, (o, s) in enumerate(results[1:], 1):
+        assert torch.equal(o, results[0][0]), f"output differs between splits (run {i})"
+        assert torch.equal(s, results[0][1]), f"state differs between splits (run {i})"
