@@ -207,3 +207,56 @@ def test_prefill_split_variants_bitwise(gpu):
     for i, (o, s) in enumerate(results[1:], 1):
         assert torch.equal(o, results[0][0]), f"output differs between splits (run {i})"
         assert torch.equal(s, results[0][1]), f"state differs between splits (run {i})"
+
+
+def test_prefill_more_sequences_than_the_sorted_schedule(gpu):
+    """More than 1,024 sequences: workgroups take sequences in natural order instead
+    of longest first.  Mostly empty sequences keep the oracle cheap."""
+    rng = np.random.default_rng(17)
+    lens = [0] * 1030
+    for i in rng.choice(1030, 24, replace=False):
+        lens[i] = int(rng.integers(1, 140))
+    say(f"prefill {len(lens)} sequences, {sum(lens)} tokens")
+    p = workloads.prefill_inputs(lens, Heads(2, 2, 4), seed=17, gate="slow", state_scale=0.5)
+    o_ref, s_ref = oracle_prefill(p)
+    out, ns = run_prefill(p, gpu)
+    torch.cuda.synchronize()
+    assert_close(host(out), o_ref, OUT_RTOL, OUT_ATOL, "output")
+    assert_close(host(ns), s_ref, STATE_RTOL, STATE_ATOL, "new_state")
+
+
+@pytest.mark.parametrize("cu_dtype", [torch.int32, torch.int64])
+def test_prefill_malformed_cu_seqlens_are_clamped(gpu, cu_dtype):
+    """Offsets are clamped on the device: sequence i covers [clamp(cu[i], 0, T),
+    clamp(cu[i+1], start, T)).  cu = [0, 40, 20, 500] with T = 100 gives [0, 40),
+    an empty sequence and [20, 100).  Tokens 20..39 belong to two sequences, so only
+    the other outputs and the three final states are compared."""
+    say(f"prefill malformed cu_seqlens {cu_dtype}")
+    T = 100
+    p = workloads.prefill_inputs([T], Heads(2, 2, 4), seed=18, gate="slow", state_scale=0.5)
+    state = 0.5 * torch.randn((3, 4, 128, 128), generator=torch.Generator().manual_seed(18))
+    bad = dict(p, state=state, cu_seqlens=torch.tensor([0, 40, 20, 500], dtype=cu_dtype))
+    out, ns = run_prefill(bad, gpu)
+    torch.cuda.synchronize()
+    for i, (s, e) in ((0, (0, 40)), (2, (20, 100))):
+        sub = {k: (p[k][s:e] if k in ("q", "k", "v", "a", "b") else p[k])
+               for k in ("q", "k", "v", "a", "b", "A_log", "dt_bias", "scale")}
+        sub["state"] = state[i:i + 1]
+        sub["cu_seqlens"] = torch.tensor([0, e - s], dtype=torch.int32)
+        o_ref, s_ref = oracle_prefill(sub)
+        keep = slice(0, 20) if i == 0 else slice(20, 80)   # tokens owned by one sequence only
+        assert_close(host(out[s:e])[keep], o_ref[keep], OUT_RTOL, OUT_ATOL, f"seq {i} output")
+        assert_close(host(ns[i]), s_ref[0], STATE_RTOL, STATE_ATOL, f"seq {i} state")
+    assert torch.equal(ns[1].cpu(), state[1]), "the empty sequence passes its state through"
+
+
+@pytest.mark.parametrize("with_state", [True, False])
+def test_prefill_no_tokens(gpu, with_state):
+    """T = 0: every sequence is empty; new_state is the initial state (or zeros)."""
+    say(f"prefill T=0 with_state={with_state}")
+    p = workloads.prefill_inputs([0, 0, 0], Heads(2, 2, 4), seed=19, with_state=with_state)
+    out, ns = run_prefill(p, gpu)
+    torch.cuda.synchronize()
+    assert out.numel() == 0
+    ref = p["state"] if with_state else torch.zeros_like(ns.cpu())
+    assert torch.equal(ns.cpu(), ref)
