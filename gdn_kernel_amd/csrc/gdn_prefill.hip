@@ -761,7 +761,11 @@ __device__ __forceinline__ void producer_loop(PrefillSmem& sm, const PrefillArgs
     // 2: the next chunk's K/Q loads; diagonal N tiles (the solve waits for
     // them); then the diagonal blocks of T~ (wave 0) or the off-diagonal N tiles
     // and one P tile each (the others).
-    if (ncs < s1) producer_prefetch(p, ncs, nclen, h, hq, hk, pt, lo, f);
+    // Split variants (few chains, a light consumer) put the solve first: the
+    // other waves issue their loads after their diagonal tile, the solve wave
+    // after its solve.
+    constexpr bool kSolveFirst = V::F > 1;
+    if (!kSolveFirst && ncs < s1) producer_prefetch(p, ncs, nclen, h, hq, hk, pt, lo, f);
     clk.lap(10);
     switch (pw) {
       case 0:
@@ -776,6 +780,7 @@ __device__ __forceinline__ void producer_loop(PrefillSmem& sm, const PrefillArgs
       case 1: {
         diag_tiles<1, 2>(sm, cb, lane);
         signal_count(sm, kDiagN, lane);
+        if (kSolveFirst && ncs < s1) producer_prefetch(p, ncs, nclen, h, hq, hk, pt, lo, f);
         const TileJob j1[2] = {{1, 1, 0}, {1, 2, 0}};
         run_tiles(sm, cb, j1, p.scale, lane);
         const TileJob j2[1] = {{2, 0, 0}};
@@ -785,6 +790,7 @@ __device__ __forceinline__ void producer_loop(PrefillSmem& sm, const PrefillArgs
       case 2: {
         diag_tiles<2, 3>(sm, cb, lane);
         signal_count(sm, kDiagN, lane);
+        if (kSolveFirst && ncs < s1) producer_prefetch(p, ncs, nclen, h, hq, hk, pt, lo, f);
         const TileJob j1[2] = {{1, 3, 0}, {1, 2, 1}};
         run_tiles(sm, cb, j1, p.scale, lane);
         const TileJob j2[1] = {{2, 1, 0}};
@@ -794,6 +800,7 @@ __device__ __forceinline__ void producer_loop(PrefillSmem& sm, const PrefillArgs
       default: {
         diag_tiles<3, 4>(sm, cb, lane);
         signal_count(sm, kDiagN, lane);
+        if (kSolveFirst && ncs < s1) producer_prefetch(p, ncs, nclen, h, hq, hk, pt, lo, f);
         const TileJob j1[2] = {{1, 3, 1}, {1, 3, 2}};
         run_tiles(sm, cb, j1, p.scale, lane);
         const TileJob j2[1] = {{2, 1, 1}};
@@ -810,6 +817,7 @@ __device__ __forceinline__ void producer_loop(PrefillSmem& sm, const PrefillArgs
     // 0 and 2, one on wave 1), V once the consumers have read the previous chunk's
     switch (pw) {
       case 0: {
+        if (kSolveFirst && ncs < s1) producer_prefetch(p, ncs, nclen, h, hq, hk, pt, lo, f);
         const TileJob j1[2] = {{2, 2, 0}, {2, 2, 1}};
         run_tiles(sm, cb, j1, p.scale, lane);
         const TileJob j2[1] = {{2, 2, 2}};
