@@ -52,6 +52,7 @@
 // leaving registers.  LDS tiles keep their contraction columns in that order
 // (perm32) so an operand row is one 16-byte read; an operand column of a
 // row-major tile is two ds_read_b64_tr_b16 (transpose reads within 16 lanes).
+#include <atomic>
 #include <type_traits>
 
 #include "gdn_common.hpp"
@@ -172,22 +173,11 @@ __device__ __forceinline__ uint2 col4_tr_plain(const uint16_t* tile, int stride,
   return read_tr(tile + (k0 + 4 * g + (j >> 2)) * stride + col0 + 4 * (j & 3));
 }
 
-
-// Operand column of the K tile: column col0 + lane%16 (of the unpermuted k
-// index), contraction rows k0 + kappa(g, s); the K tile form of frag_tr.
-__device__ __forceinline__ uint2 col4_tr_k(const uint16_t* tile, int k0, int col0, int lane) {
-  const int j = lane & 15, g = lane >> 4;
-  return read_tr(tile + kq_off(k0 + 4 * g + (j >> 2), perm(col0 + 4 * (j & 3))));
-}
-__device__ __forceinline__ uint4 frag_tr_k(const uint16_t* tile, int k0, int col0, int lane) {
-  const uint2 a = col4_tr_k(tile, k0, col0, lane);
-  const uint2 b = col4_tr_k(tile, k0 + 16, col0, lane);
-  return uint4{a.x, a.y, b.x, b.y};
-}
-
-// The same reads with the address split into lane bases and constants.  For
-// k0 a multiple of 16 and col0 = 16 kt, col4_tr_k reads element
-//   kq_off(k0 + rl, perm(16 kt + 4 (j & 3))),  rl = 4 g + j / 4,
+// Operand column of the K tile for the state update: column 16 kt + lane%16 (of
+// the unpermuted k index), contraction rows 32 ks + kappa(g, s), as two
+// transpose reads of 4 rows (k0 = 32 ks, then k0 + 16).  In 16-lane group g lane
+// j reads 4 contiguous columns of row k0 + rl, rl = 4 g + j / 4, namely element
+//   kq_off(k0 + rl, perm(16 kt + 4 (j & 3))),
 // and perm(16 kt + 4 (j & 3)) = 32 (kt / 2) + 8 (j & 3) + 4 (kt & 1), so with
 // s = sigma(rl) the offset is
 //   (k0 + rl) KSTR + 32 ((kt / 2) ^ (s >> 2)) + 8 ((j & 3) ^ (s & 3)) + 4 (kt & 1):
@@ -1149,15 +1139,15 @@ hipError_t launch_variant(const PrefillArgs& a, hipStream_t stream) {
 
 // Compute units of the current device (queried once per device).
 int device_cus() {
-  static int cus[64] = {0};
+  static std::atomic<int> cus[64];  // 0 until queried; racing first queries store the same value
   int dev = 0;
   if (hipGetDevice(&dev) != hipSuccess || dev < 0 || dev >= 64) return 256;
-  if (cus[dev] == 0) {
-    int n = 0;
+  int n = cus[dev].load(std::memory_order_relaxed);
+  if (n == 0) {
     if (hipDeviceGetAttribute(&n, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || n <= 0) n = 256;
-    cus[dev] = n;
+    cus[dev].store(n, std::memory_order_relaxed);
   }
-  return cus[dev];
+  return n;
 }
 
 }  // namespace
