@@ -19,7 +19,8 @@ GDN_ERR_DEVICE = 3
 GDN_INDEX_INT32 = 0
 GDN_INDEX_INT64 = 1
 
-# Exported symbols and their argument types (must match include/gdn_kernel_amd.h).
+# Exported symbols and their argument types (must match include/gdn_kernel_amd.h and
+# include/gdn_kernel_amd_testing.h).
 _P = c_void_p
 _HEADS = [c_int32, c_int32, c_int32, c_int32, c_int32]
 SIGNATURES = {
@@ -35,6 +36,9 @@ SIGNATURES = {
                     c_int),
     "gdn_prefill_check": ([_P] * 8 + [_P, c_int32, c_int64, c_int64, c_double, _P, _P] + _HEADS,
                           c_int),
+    # include/gdn_kernel_amd_testing.h
+    "gdn_prefill_fault_injection": ([_P] * 8 + [_P, c_int32, c_int64, c_int64, c_double, _P, _P]
+                                    + _HEADS + [c_int32, c_int32, _P, _P], c_int),
 }
 
 _lib = None

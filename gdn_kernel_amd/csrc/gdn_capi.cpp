@@ -8,6 +8,7 @@
 #include <cstring>
 
 #include "../../include/gdn_kernel_amd.h"
+#include "../../include/gdn_kernel_amd_testing.h"
 #include "gdn_launch.hpp"
 
 namespace {
@@ -177,16 +178,24 @@ int gdn_prefill_check(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v, c
   return ok();
 }
 
-int gdn_prefill(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v, const float* state, const float* A_log,
-                const gdn_bf16* a, const float* dt_bias, const gdn_bf16* b, const void* cu_seqlens,
-                int32_t cu_seqlens_dtype, int64_t num_seqs, int64_t total_tokens, double scale, gdn_bf16* output,
-                float* new_state, int32_t num_q_heads, int32_t num_k_heads, int32_t num_v_heads,
-                int32_t head_dim_k, int32_t head_dim_v, void* stream) {
+}  // extern "C"
+
+namespace {
+
+int prefill_impl(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v, const float* state, const float* A_log,
+                 const gdn_bf16* a, const float* dt_bias, const gdn_bf16* b, const void* cu_seqlens,
+                 int32_t cu_seqlens_dtype, int64_t num_seqs, int64_t total_tokens, double scale, gdn_bf16* output,
+                 float* new_state, int32_t num_q_heads, int32_t num_k_heads, int32_t num_v_heads,
+                 int32_t head_dim_k, int32_t head_dim_v, int32_t spin_limit, int32_t ready_chunks,
+                 uint32_t* aborts, void* stream) {
   GDN_TRY(gdn_prefill_check(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu_seqlens_dtype, num_seqs,
                             total_tokens, scale, output, new_state, num_q_heads, num_k_heads, num_v_heads,
                             head_dim_k, head_dim_v));
   if (num_seqs == 0) return ok();
   gdn::PrefillArgs args{};
+  args.spin_limit = spin_limit;
+  args.ready_chunks = ready_chunks;
+  args.aborts = aborts;
   args.q = q; args.k = k; args.v = v;
   args.state = state; args.new_state = new_state;
   args.A_log = A_log; args.a = a; args.dt_bias = dt_bias; args.b = b;
@@ -196,6 +205,35 @@ int gdn_prefill(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v, const f
   args.T = total_tokens;
   args.N = int(num_seqs); args.Hq = num_q_heads; args.Hk = num_k_heads; args.Hv = num_v_heads;
   return device_status(gdn::launch_prefill(args, static_cast<hipStream_t>(stream)), "gdn_prefill launch");
+}
+
+}  // namespace
+
+extern "C" {
+
+int gdn_prefill(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v, const float* state, const float* A_log,
+                const gdn_bf16* a, const float* dt_bias, const gdn_bf16* b, const void* cu_seqlens,
+                int32_t cu_seqlens_dtype, int64_t num_seqs, int64_t total_tokens, double scale, gdn_bf16* output,
+                float* new_state, int32_t num_q_heads, int32_t num_k_heads, int32_t num_v_heads,
+                int32_t head_dim_k, int32_t head_dim_v, void* stream) {
+  return prefill_impl(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu_seqlens_dtype, num_seqs, total_tokens,
+                      scale, output, new_state, num_q_heads, num_k_heads, num_v_heads, head_dim_k, head_dim_v, 0, 0,
+                      nullptr, stream);
+}
+
+int gdn_prefill_fault_injection(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v, const float* state,
+                                const float* A_log, const gdn_bf16* a, const float* dt_bias, const gdn_bf16* b,
+                                const void* cu_seqlens, int32_t cu_seqlens_dtype, int64_t num_seqs,
+                                int64_t total_tokens, double scale, gdn_bf16* output, float* new_state,
+                                int32_t num_q_heads, int32_t num_k_heads, int32_t num_v_heads, int32_t head_dim_k,
+                                int32_t head_dim_v, int32_t spin_limit, int32_t ready_chunks, uint32_t* aborts,
+                                void* stream) {
+  if (spin_limit < 0 || ready_chunks < 0)
+    return fail(GDN_ERR_INVALID_ARGUMENT, "spin_limit and ready_chunks must be >= 0 (got %d, %d)", spin_limit,
+                ready_chunks);
+  return prefill_impl(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu_seqlens_dtype, num_seqs, total_tokens,
+                      scale, output, new_state, num_q_heads, num_k_heads, num_v_heads, head_dim_k, head_dim_v,
+                      spin_limit, ready_chunks, aborts, stream);
 }
 
 }  // extern "C"

@@ -40,6 +40,10 @@ struct PrefillArgs {
   float scale;
   int64_t T;                // total packed tokens
   int N, Hq, Hk, Hv;
+  // Testing hooks for the hand-off failure path (zero in production launches):
+  int spin_limit;           // polls before a hand-off wait gives up; 0 => the default (~70 ms)
+  int ready_chunks;         // > 0: producers signal "chunk ready" only for chunks < ready_chunks
+  unsigned* aborts;         // non-null: +1 (device atomic) each time a wait gives up
 };
 
 hipError_t launch_decode(const DecodeArgs& args, hipStream_t stream);

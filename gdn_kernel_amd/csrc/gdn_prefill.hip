@@ -74,8 +74,9 @@ constexpr int TSTR = 72;     // bf16 row stride of 64-wide tiles (T~, P, N)
 constexpr int NDB = 16 * 16 + 4;  // floats per diagonal N block (column-major; padded by 16 bytes)
 constexpr int NROWS = C - 16;  // rows of N kept for the off-diagonal solve
 
-template <int NCW_, int VT_>
+template <int NCW_, int VT_, bool HOOKS_ = false>
 struct Variant {
+  static constexpr bool kHooks = HOOKS_;         // testing hooks of PrefillArgs compiled in
   static constexpr int NCW = NCW_;               // consumer waves
   static constexpr int VT = VT_;                 // 16-row state tiles per consumer wave
   static constexpr int VW = 16 * VT;             // state rows per consumer wave
@@ -103,6 +104,8 @@ struct __align__(16) PrefillSmem {
   float dd[2][C];             // e^{gamma_last - gamma_c}
   int seq;                    // sequence handled by this workgroup
   int sync[8];                // hand-off counters (kReady, kVFree, kConsumed, kPPhase, kAbort, kDiagN, kX32)
+  int spin_limit;             // kernels with testing hooks: polls before a hand-off wait gives up
+  unsigned* aborts;           // kernels with testing hooks: optional count of waits that gave up
 };
 
 constexpr float kLog2e = 1.4426950408889634f;
@@ -277,7 +280,7 @@ __device__ __forceinline__ void wave_lds_sync() {
 // signals by adding 1 after all its earlier LDS accesses completed (release); a
 // waiter polls until the count reaches its target (acquire).
 enum SyncCounter { kReady = 0, kVFree = 1, kConsumed = 2, kPPhase = 3, kAbort = 4, kDiagN = 5, kX32 = 6 };
-constexpr int kSpinLimit = 1 << 21;  // polls (about 70 ms) before a wait gives up
+constexpr int kSpinLimit = 1 << 21;  // default polls (about 70 ms) before a wait gives up
 
 __device__ __forceinline__ void signal_count(PrefillSmem& sm, int which, int lane) {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
@@ -285,17 +288,25 @@ __device__ __forceinline__ void signal_count(PrefillSmem& sm, int which, int lan
 }
 
 // Waits until counter `which` reaches `target`.  Every wait is bounded: if one
-// ever gives up (which only a logic error could cause), it raises kAbort and all
-// later waits return at once, so the workgroup still finishes (with wrong
-// results) instead of hanging.
+// ever gives up (which only a logic error, or the testing hooks of PrefillArgs,
+// can cause), it raises kAbort, and all later waits return at once, so the
+// workgroup still finishes (with wrong results) instead of hanging.  Production
+// kernels give up after kSpinLimit polls; kernels built with the hooks after
+// sm.spin_limit polls, counting each give-up in sm.aborts if set.
+template <bool kHooks>
 __device__ __forceinline__ void wait_count(PrefillSmem& sm, int which, int target) {
   if (__hip_atomic_load(&sm.sync[which], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < target) {
     for (int it = 0;; ++it) {
       __builtin_amdgcn_s_sleep(1);
       if (__hip_atomic_load(&sm.sync[which], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) >= target) break;
       if (__hip_atomic_load(&sm.sync[kAbort], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != 0) break;
-      if (it >= kSpinLimit) {
+      if (it >= (kHooks ? sm.spin_limit : kSpinLimit)) {
         __hip_atomic_store(&sm.sync[kAbort], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+        if constexpr (kHooks) {
+          unsigned* aborts = sm.aborts;
+          if (aborts && __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)) == 0)
+            __hip_atomic_fetch_add(aborts, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        }
         break;
       }
     }
@@ -605,6 +616,7 @@ __device__ __forceinline__ void offdiag_right(PrefillSmem& sm, const ChunkBufs& 
   (void)t;
 }
 
+template <bool kHooks>
 __device__ __forceinline__ void offdiag_left(PrefillSmem& sm, const ChunkBufs& cb, int t, int lane) {
   const Pair2 d0 = diag_b(cb, 0, lane);
   const Pair2 a1 = block_a(cb.Th, cb.Tl, 0, 1, 1, lane), a2 = block_a(cb.Th, cb.Tl, 0, 2, 2, lane),
@@ -621,7 +633,7 @@ __device__ __forceinline__ void offdiag_left(PrefillSmem& sm, const ChunkBufs& c
   const Pair2 nm30 = acc_b(-mul3_16(p30, n31, b10));
   store_block(cb, mul3_16(zero4(), a2, nm20), 2, 0, lane);  // X20
   const f32x4 x30 = mul3_16(zero4(), a3, nm30);
-  wait_count(sm, kX32, t + 1);  // X32 stored by the right wave
+  wait_count<kHooks>(sm, kX32, t + 1);  // X32 stored by the right wave
   const Pair2 x32 = block_a(cb.Th, cb.Tl, 0, 3, 2, lane);
   store_block(cb, mul3_16(x30, x32, nm20), 3, 0, lane);     // X30
 }
@@ -706,7 +718,7 @@ __device__ __forceinline__ void producer_loop(PrefillSmem& sm, const PrefillArgs
     const int64_t ncs = cs + C;
     const int nclen = int(s1 - ncs < C ? s1 - ncs : C);
     const ChunkBufs cb = chunk_bufs(sm, t & 1);
-    if (t >= 2) wait_count(sm, kConsumed, V::NCW * (t - 1));  // chunk t - 2 consumed
+    if (t >= 2) wait_count<V::kHooks>(sm, kConsumed, V::NCW * (t - 1));  // chunk t - 2 consumed
     clk.lap(0);
 
     // 1: stage K/Q (permuted columns), gates
@@ -742,7 +754,7 @@ __device__ __forceinline__ void producer_loop(PrefillSmem& sm, const PrefillArgs
     }
     clk.lap(1);
     signal_count(sm, kPPhase, lane);
-    wait_count(sm, kPPhase, 4 * (2 * t + 1));  // all of K/Q/gates staged
+    wait_count<V::kHooks>(sm, kPPhase, 4 * (2 * t + 1));  // all of K/Q/gates staged
     clk.lap(2);
     // The rest of the chunk is the longer chain: producer waves go ahead of the
     // consumer wave sharing the SIMD.
@@ -762,7 +774,7 @@ __device__ __forceinline__ void producer_loop(PrefillSmem& sm, const PrefillArgs
         diag_tiles<0, 1>(sm, cb, lane);
         signal_count(sm, kDiagN, lane);
         clk.lap(3);
-        wait_count(sm, kDiagN, 4 * (t + 1));
+        wait_count<V::kHooks>(sm, kDiagN, 4 * (t + 1));
         clk.lap(4);
         diag_solve(sm, cb, lane);
         clk.lap(5);
@@ -800,7 +812,7 @@ __device__ __forceinline__ void producer_loop(PrefillSmem& sm, const PrefillArgs
     }
     clk.lap(3);
     signal_count(sm, kPPhase, lane);
-    wait_count(sm, kPPhase, 4 * (2 * t + 2));  // diagonal blocks and N tiles done
+    wait_count<V::kHooks>(sm, kPPhase, 4 * (2 * t + 2));  // diagonal blocks and N tiles done
     clk.lap(6);
 
     // 3: off-diagonal blocks of T~ (waves 1 and 3), the remaining P tiles (waves
@@ -828,11 +840,11 @@ __device__ __forceinline__ void producer_loop(PrefillSmem& sm, const PrefillArgs
         break;
       }
       default:
-        offdiag_left(sm, cb, t, lane);
+        offdiag_left<V::kHooks>(sm, cb, t, lane);
         break;
     }
     clk.lap(7);
-    if (t >= 1) wait_count(sm, kVFree, V::NCW * t);
+    if (t >= 1) wait_count<V::kHooks>(sm, kVFree, V::NCW * t);
     clk.lap(8);
 #pragma unroll
     for (int it = 0; it < NVIT; ++it) {
@@ -841,7 +853,7 @@ __device__ __forceinline__ void producer_loop(PrefillSmem& sm, const PrefillArgs
         *reinterpret_cast<uint4*>(sm.V + (seg / (V::ROWS / 8)) * VSTR + 8 * (seg % (V::ROWS / 8))) = fv[it];
     }
     __builtin_amdgcn_s_setprio(0);
-    signal_count(sm, kReady, lane);
+    if (!V::kHooks || p.ready_chunks <= 0 || t < p.ready_chunks) signal_count(sm, kReady, lane);
     clk.lap(9);
   }
   clk.store(V::NCW + pw, lane0);
@@ -903,7 +915,7 @@ __device__ __forceinline__ void consumer_loop(PrefillSmem& sm, const PrefillArgs
     const int64_t cs = s0 + int64_t(t - 1) * C;
     const int clen = int(s1 - cs < C ? s1 - cs : C);
     const ChunkBufs cb = chunk_bufs(sm, (t - 1) & 1);
-    wait_count(sm, kReady, 4 * t);  // chunk t - 1 prepared
+    wait_count<V::kHooks>(sm, kReady, 4 * t);  // chunk t - 1 prepared
     clk.lap(0);
 
     // 1: X = K S^T, (Q S^T)^T
@@ -1087,6 +1099,10 @@ __global__ __launch_bounds__(V::NTHREADS) void gdn_prefill_kernel(PrefillArgs p)
       }
     }
     if (tid < 8) sm.sync[tid] = 0;
+    if (V::kHooks && tid == 0) {
+      sm.spin_limit = p.spin_limit > 0 ? p.spin_limit : kSpinLimit;
+      sm.aborts = p.aborts;
+    }
   }
   __syncthreads();  // cleared LDS and counters visible to both roles
 
@@ -1163,6 +1179,16 @@ hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream) {
   const int64_t cus = device_cus();
   int F = 1;
   while (F < GDN_PREFILL_MAX_SPLIT && chains * 2 * F <= cus) F *= 2;
+  // Launches that use the testing hooks get kernels with the hooks compiled in;
+  // production launches keep them out of the device code.
+  if (a.spin_limit != 0 || a.ready_chunks != 0 || a.aborts != nullptr) {
+    switch (F) {
+      case 1: return launch_variant<Variant<4, 2, true>>(a, stream);
+      case 2: return launch_variant<Variant<2, 2, true>>(a, stream);
+      case 4: return launch_variant<Variant<1, 2, true>>(a, stream);
+      default: return launch_variant<Variant<1, 1, true>>(a, stream);
+    }
+  }
   switch (F) {
     case 1: return launch_variant<Variant<4, 2>>(a, stream);
     case 2: return launch_variant<Variant<2, 2>>(a, stream);

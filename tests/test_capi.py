@@ -11,15 +11,18 @@ import pytest
 from gdn_kernel_amd import _lib
 
 ROOT = Path(__file__).resolve().parents[1]
-HEADER = ROOT / "include" / "gdn_kernel_amd.h"
+HEADERS = sorted((ROOT / "include").glob("*.h"))
 
 OK, INVALID, UNSUPPORTED = _lib.GDN_OK, _lib.GDN_ERR_INVALID_ARGUMENT, _lib.GDN_ERR_UNSUPPORTED
 FAKE = 0x10000  # non-null, never dereferenced by the *_check functions
 
 
 def header_functions():
-    text = re.sub(r"/\*.*?\*/", "", HEADER.read_text(), flags=re.S)
-    return sorted(set(re.findall(r"\b(gdn_[a-z_0-9]+)\s*\(", text)))
+    names = set()
+    for h in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", h.read_text(), flags=re.S)
+        names |= set(re.findall(r"\b(gdn_[a-z_0-9]+)\s*\(", text))
+    return sorted(names)
 
 
 @pytest.fixture(scope="module")

@@ -4,7 +4,7 @@ import numpy as np
 import pytest
 import torch
 
-from gdn_kernel_amd import binding, workloads
+from gdn_kernel_amd import _lib, binding, workloads
 from gdn_kernel_amd.workloads import Heads, to_numpy
 from oracle import gdn_oracle as O
 from tests.conftest import assert_close
@@ -260,3 +260,53 @@ def test_prefill_no_tokens(gpu, with_state):
     assert out.numel() == 0
     ref = p["state"] if with_state else torch.zeros_like(ns.cpu())
     assert torch.equal(ns.cpu(), ref)
+
+
+def _prefill_fault_injection(p, gpu, spin_limit, ready_chunks):
+    """gdn_prefill_fault_injection through the C ABI; returns (output, new_state, aborts)."""
+    d = {k: (v.to(gpu) if isinstance(v, torch.Tensor) else v) for k, v in p.items()}
+    T, Hq = d["q"].shape[0], d["q"].shape[1]
+    Hk, Hv = d["k"].shape[1], d["v"].shape[1]
+    cu = d["cu_seqlens"]
+    N = cu.numel() - 1
+    out = torch.full((T, Hv, 128), float("nan"), device=gpu, dtype=torch.bfloat16)
+    ns = torch.full((N, Hv, 128, 128), float("nan"), device=gpu, dtype=torch.float32)
+    aborts = torch.zeros(1, device=gpu, dtype=torch.int32)
+    cu_code = _lib.GDN_INDEX_INT32 if cu.dtype == torch.int32 else _lib.GDN_INDEX_INT64
+    ptr = lambda t: None if t is None else t.data_ptr()
+    rc = _lib.load().gdn_prefill_fault_injection(
+        ptr(d["q"]), ptr(d["k"]), ptr(d["v"]), ptr(d["state"]), ptr(d["A_log"]), ptr(d["a"]),
+        ptr(d["dt_bias"]), ptr(d["b"]), cu.data_ptr(), cu_code, N, T, d["scale"], ptr(out), ptr(ns),
+        Hq, Hk, Hv, 128, 128, spin_limit, ready_chunks, ptr(aborts),
+        torch.cuda.current_stream(gpu).cuda_stream)
+    _lib.check(rc)
+    return out, ns, aborts
+
+
+def test_prefill_bounded_waits(gpu):
+    """The hand-off failure path, forced from the host.  With the testing hooks off
+    the entry point is gdn_prefill bit for bit.  With the producers signalling only
+    their first chunk and a 2,000-poll wait limit, every workgroup of a sequence with
+    two or more chunks has a consumer wait that can only give up: the launch still
+    completes (every wait is bounded), the give-ups are counted, the one-chunk
+    sequence's results are untouched, and the next normal launch is exact again."""
+    lens = [300, 130, 40]             # 5, 3 and 1 chunks; 96 chains: split 2 ways
+    p = workloads.prefill_inputs(lens, seed=21, gate="slow", state_scale=0.5)
+    say("prefill bounded waits: hooks off")
+    o0, s0, a0 = _prefill_fault_injection(p, gpu, 0, 0)
+    o1, s1 = run_prefill(p, gpu)
+    torch.cuda.synchronize()
+    assert int(a0.item()) == 0
+    assert torch.equal(o0, o1) and torch.equal(s0, s1)
+    say("prefill bounded waits: chunk-ready signals stop after chunk 0, 2000-poll limit")
+    o2, s2, a2 = _prefill_fault_injection(p, gpu, 2000, 1)
+    torch.cuda.synchronize()
+    waiting_wgs = 2 * 32 * 2          # sequences with >= 2 chunks x v-heads x workgroups per chain
+    n = int(a2.item())
+    assert waiting_wgs <= n <= waiting_wgs * 8, n
+    s, e = sum(lens[:2]), sum(lens)
+    assert torch.equal(o2[s:e], o1[s:e]) and torch.equal(s2[2], s1[2])
+    say("prefill bounded waits: a normal launch afterwards")
+    o3, s3 = run_prefill(p, gpu)
+    torch.cuda.synchronize()
+    assert torch.equal(o3, o1) and torch.equal(s3, s1)
