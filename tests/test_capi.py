@@ -134,6 +134,20 @@ def test_prefill_rejects(lib, kw, code, frag):
     assert lib.gdn_prefill(*pre_args(**kw), None) == code
 
 
+@pytest.mark.parametrize("kw,code,frag", [
+    (dict(N=-1), INVALID, "num_seqs"),
+    (dict(dk=96), UNSUPPORTED, "128"),
+])
+def test_prefill_fault_injection_rejects(lib, kw, code, frag):
+    """The testing entry point validates like gdn_prefill, and its hooks must be >= 0;
+    every case fails before any device call."""
+    assert lib.gdn_prefill_fault_injection(*pre_args(**kw), 0, 0, None, None) == code
+    assert frag in _lib.last_error()
+    for spin, ready in ((-1, 0), (0, -2)):
+        assert lib.gdn_prefill_fault_injection(*pre_args(), spin, ready, None, None) == INVALID
+        assert "spin_limit" in _lib.last_error()
+
+
 def test_last_error_is_cleared_on_success(lib):
     lib.gdn_decode_check(*dec_args(B=-1))
     assert _lib.last_error()
