@@ -209,18 +209,42 @@ __device__ __forceinline__ uint4 pack_hi(const f32x4& t0, const f32x4& t1) {
   return uint4{pack_bf16x2(t0[0], t0[1]), pack_bf16x2(t0[2], t0[3]), pack_bf16x2(t1[0], t1[1]),
                pack_bf16x2(t1[2], t1[3])};
 }
-// bf16 lo parts x - hi(x) (exact in fp32), rounded to bf16, given the hi word.
-__device__ __forceinline__ uint32_t lo_word(float a, float b, uint32_t hi) {
-  return pack_bf16x2(a - bf16lo_f32(hi), b - bf16hi_f32(hi));
+
+// 16x16x16 MFMA (one 16-wide contraction block): lane l supplies A[l%16][4g..4g+3]
+// and B[4g..4g+3][l%16], g = l/16 -- the lower half of the 32-wide convention.
+__device__ __forceinline__ f32x4 mfma16(const uint2& a, const uint2& b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4, a), __builtin_bit_cast(i16x4, b), c, 0,
+                                                   0, 0);
 }
+
+// The residuals t - hi(t) of four fp32 values per lane, given their bf16 hi parts
+// packed as a 16x16x16 B operand (lane l, slot s: B[4g + s][l%16]), formed on the
+// matrix pipe: D = t + (-I) hi(t) with t as the accumulator, which lane l holds as
+// D[4g + s][l%16] -- the same (lane, slot) for every element, so this is an
+// elementwise t - hi(t).  Each element has one nonzero product and its exact result
+// is representable, so the residual is exact (as the fp32 subtraction would be),
+// and the wave issues one MFMA instead of eight VALU instructions.  -I as the A
+// operand (lane l: row l%16, contraction 4g + s) has its one nonzero, bf16 -1, in
+// slot l%4 when g == (l%16)/4.
+__device__ __forceinline__ f32x4 residual4(const f32x4& t, const uint2& hi) {
+  const uint32_t l = __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u));
+  const uint32_t w = (l >> 4) == ((l & 15) >> 2) ? (0xbf80u << (16 * (l & 1))) : 0u;
+  const uint2 neg_identity = (l & 2) ? uint2{0u, w} : uint2{w, 0u};
+  return mfma16(neg_identity, hi, t);
+}
+
+// bf16 hi parts (round to nearest even) and lo parts (the residual, rounded) of
+// two stacked accumulator tiles (B/A operands, as pack_hi) or of one.
 __device__ __forceinline__ void split_pack(const f32x4& t0, const f32x4& t1, uint4& hi, uint4& lo) {
   hi = pack_hi(t0, t1);
-  lo = uint4{lo_word(t0[0], t0[1], hi.x), lo_word(t0[2], t0[3], hi.y), lo_word(t1[0], t1[1], hi.z),
-             lo_word(t1[2], t1[3], hi.w)};
+  const f32x4 r0 = residual4(t0, uint2{hi.x, hi.y}), r1 = residual4(t1, uint2{hi.z, hi.w});
+  lo = uint4{pack_bf16x2(r0[0], r0[1]), pack_bf16x2(r0[2], r0[3]), pack_bf16x2(r1[0], r1[1]),
+             pack_bf16x2(r1[2], r1[3])};
 }
 __device__ __forceinline__ void split4(const f32x4& t, uint2& hi, uint2& lo) {
   hi = uint2{pack_bf16x2(t[0], t[1]), pack_bf16x2(t[2], t[3])};
-  lo = uint2{lo_word(t[0], t[1], hi.x), lo_word(t[2], t[3], hi.y)};
+  const f32x4 r = residual4(t, hi);
+  lo = uint2{pack_bf16x2(r[0], r[1]), pack_bf16x2(r[2], r[3])};
 }
 
 __device__ __forceinline__ int64_t load_cu(const void* cu, int is64, int i) {
@@ -529,13 +553,6 @@ __device__ __forceinline__ void diag_solve(PrefillSmem& sm, const ChunkBufs& cb,
       cb.Tl[(16 * r + 4 * q + e) * TSTR + colp] = uint16_t(l4[e]);
     }
   }
-}
-
-// 16x16x16 MFMA (one 16-wide contraction block): lane l supplies A[l%16][4g..4g+3]
-// and B[4g..4g+3][l%16], g = l/16 -- the lower half of the 32-wide convention.
-__device__ __forceinline__ f32x4 mfma16(const uint2& a, const uint2& b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(__builtin_bit_cast(i16x4, a), __builtin_bit_cast(i16x4, b), c, 0,
-                                                   0, 0);
 }
 
 struct Pair2 {  // bf16 hi / lo parts of a 16x16x16 operand
