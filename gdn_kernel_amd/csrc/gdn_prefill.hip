@@ -2,10 +2,10 @@
 //
 // A workgroup walks the chunks of one (sequence, v-head) chain, or of one slice
 // of its state rows, as a two-stage pipeline:
-//   * producer waves 4-7 prepare chunk t: stage K and Q in LDS, form the gates,
-//     the masked/decayed products N = strictLower(beta Gamma KK^T) and
-//     P = tril(Gamma QK^T), and T~ = (I + N)^-1;
-//   * consumer waves 0-3 meanwhile advance the state through chunk t-1.
+//   * four producer waves (NCW .. NCW+3) prepare chunk t: stage K and Q in LDS,
+//     form the gates, the masked/decayed products N = strictLower(beta Gamma KK^T)
+//     and P = tril(Gamma QK^T), and T~ = (I + N)^-1;
+//   * the consumer waves (0 .. NCW-1) meanwhile advance the state through chunk t-1.
 // Every LDS buffer a consumer reads (K, Q, T~, P, gates) is double-buffered by
 // chunk parity (V is single-buffered and rewritten only after it was read).
 // The roles hand chunks over through LDS counters, so each runs its own chain
@@ -33,16 +33,17 @@
 //   o  = scale (e^gamma Q S^T + P v_new)              (:216-234, 273-283)
 //   S  = e^{gamma_last} S + (d v_new)^T K,  d_c = e^{gamma_last - gamma_c}   (:197-202, 286-293)
 //
-// T~ is built in two steps: each producer wave inverts one diagonal 16x16 block
-// by forward substitution (four lanes per column, partial sums combined across
-// rows with permlane swaps), then one wave forms the off-diagonal blocks by the
-// block recursion X_IJ = -D_I sum_K N_IK X_KJ on MFMA, keeping the X blocks it
-// needs later in registers.
+// T~ is built in three steps: each producer wave forms one diagonal 16x16 tile of
+// N; one wave inverts the four diagonal blocks D_I = (I + N_II)^-1 by forward
+// substitution (16 lanes per block, one lane per column); two waves then form the
+// off-diagonal blocks as a 2x2 block inverse over the 32x32 halves on 16x16x16
+// MFMAs (offdiag_right / offdiag_left).
 //
 // Precision: q/k/v are exact bf16 MFMA operands.  Operands that are fp32 values
 // (S, Y, N, T~, d*v_new) are split into bf16 hi + lo pairs so that the products
 // feeding the state carry ~16 mantissa bits; fp32 accumulation throughout.  The
-// output-only products (Q S^T and P v_new) use bf16 hi parts alone.
+// output-only products (Q S^T and P v_new) use bf16 hi parts alone.  The residual
+// x - hi(x) of a split is formed exactly on the matrix pipe (residual4).
 //
 // MFMA operand convention (v_mfma_f32_16x16x32_bf16): lane l supplies row/col
 // l%16 and 8 contraction elements chosen by g = l/16.  A and B are paired with
@@ -397,7 +398,7 @@ __device__ __forceinline__ ChunkBufs chunk_bufs(PrefillSmem& sm, int b) {
 }
 
 // ---------------------------------------------------------------------------
-// Producer side (waves 4-7)
+// Producer side (waves NCW .. NCW+3)
 // ---------------------------------------------------------------------------
 
 // Tiles of N and P from the staged K and Q (16x16 tiles, 4 MFMAs each).
