@@ -98,24 +98,6 @@ int gdn_decode_check(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v, co
   return ok();
 }
 
-int gdn_decode(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v, const float* state,
-               const float* A_log, const gdn_bf16* a, const float* dt_bias, const gdn_bf16* b, double scale,
-               gdn_bf16* output, float* new_state, int64_t batch, int32_t num_q_heads, int32_t num_k_heads,
-               int32_t num_v_heads, int32_t head_dim_k, int32_t head_dim_v, void* stream) {
-  GDN_TRY(gdn_decode_check(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state, batch, num_q_heads,
-                           num_k_heads, num_v_heads, head_dim_k, head_dim_v));
-  if (batch == 0) return ok();
-  gdn::DecodeArgs args{};
-  args.q = q; args.k = k; args.v = v;
-  args.state = state; args.new_state = new_state;
-  args.A_log = A_log; args.a = a; args.dt_bias = dt_bias; args.b = b;
-  args.slots = nullptr; args.pool_slots = 0;
-  args.out = output;
-  args.scale = resolve_scale(scale);
-  args.B = int(batch); args.Hq = num_q_heads; args.Hk = num_k_heads; args.Hv = num_v_heads;
-  return device_status(gdn::launch_decode(args, static_cast<hipStream_t>(stream)), "gdn_decode launch");
-}
-
 int gdn_decode_pooled_check(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v, float* state_pool,
                             int64_t pool_slots, const int32_t* state_indices, const float* A_log,
                             const gdn_bf16* a, const float* dt_bias, const gdn_bf16* b, double scale,
@@ -131,25 +113,6 @@ int gdn_decode_pooled_check(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16
   if (batch * num_v_heads * (kD / 8) > kMaxGrid)
     return fail(GDN_ERR_INVALID_ARGUMENT, "batch * num_v_heads too large (%lld)", (long long)(batch * num_v_heads));
   return ok();
-}
-
-int gdn_decode_pooled(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v, float* state_pool,
-                      int64_t pool_slots, const int32_t* state_indices, const float* A_log, const gdn_bf16* a,
-                      const float* dt_bias, const gdn_bf16* b, double scale, gdn_bf16* output, int64_t batch,
-                      int32_t num_q_heads, int32_t num_k_heads, int32_t num_v_heads, int32_t head_dim_k,
-                      int32_t head_dim_v, void* stream) {
-  GDN_TRY(gdn_decode_pooled_check(q, k, v, state_pool, pool_slots, state_indices, A_log, a, dt_bias, b, scale,
-                                  output, batch, num_q_heads, num_k_heads, num_v_heads, head_dim_k, head_dim_v));
-  if (batch == 0) return ok();
-  gdn::DecodeArgs args{};
-  args.q = q; args.k = k; args.v = v;
-  args.state = state_pool; args.new_state = state_pool;
-  args.A_log = A_log; args.a = a; args.dt_bias = dt_bias; args.b = b;
-  args.slots = state_indices; args.pool_slots = pool_slots;
-  args.out = output;
-  args.scale = resolve_scale(scale);
-  args.B = int(batch); args.Hq = num_q_heads; args.Hk = num_k_heads; args.Hv = num_v_heads;
-  return device_status(gdn::launch_decode(args, static_cast<hipStream_t>(stream)), "gdn_decode_pooled launch");
 }
 
 int gdn_prefill_check(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v, const float* state,
@@ -182,6 +145,44 @@ int gdn_prefill_check(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v, c
 
 namespace {
 
+int decode_impl(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v, const float* state,
+                const float* A_log, const gdn_bf16* a, const float* dt_bias, const gdn_bf16* b, double scale,
+                gdn_bf16* output, float* new_state, int64_t batch, int32_t num_q_heads, int32_t num_k_heads,
+                int32_t num_v_heads, int32_t head_dim_k, int32_t head_dim_v, int variant, void* stream) {
+  GDN_TRY(gdn_decode_check(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state, batch, num_q_heads,
+                           num_k_heads, num_v_heads, head_dim_k, head_dim_v));
+  if (batch == 0) return ok();
+  gdn::DecodeArgs args{};
+  args.q = q; args.k = k; args.v = v;
+  args.state = state; args.new_state = new_state;
+  args.A_log = A_log; args.a = a; args.dt_bias = dt_bias; args.b = b;
+  args.slots = nullptr; args.pool_slots = 0;
+  args.out = output;
+  args.scale = resolve_scale(scale);
+  args.B = int(batch); args.Hq = num_q_heads; args.Hk = num_k_heads; args.Hv = num_v_heads;
+  return device_status(gdn::launch_decode(args, static_cast<hipStream_t>(stream), variant), "gdn_decode launch");
+}
+
+int decode_pooled_impl(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v, float* state_pool,
+                       int64_t pool_slots, const int32_t* state_indices, const float* A_log, const gdn_bf16* a,
+                       const float* dt_bias, const gdn_bf16* b, double scale, gdn_bf16* output, int64_t batch,
+                       int32_t num_q_heads, int32_t num_k_heads, int32_t num_v_heads, int32_t head_dim_k,
+                       int32_t head_dim_v, int variant, void* stream) {
+  GDN_TRY(gdn_decode_pooled_check(q, k, v, state_pool, pool_slots, state_indices, A_log, a, dt_bias, b, scale,
+                                  output, batch, num_q_heads, num_k_heads, num_v_heads, head_dim_k, head_dim_v));
+  if (batch == 0) return ok();
+  gdn::DecodeArgs args{};
+  args.q = q; args.k = k; args.v = v;
+  args.state = state_pool; args.new_state = state_pool;
+  args.A_log = A_log; args.a = a; args.dt_bias = dt_bias; args.b = b;
+  args.slots = state_indices; args.pool_slots = pool_slots;
+  args.out = output;
+  args.scale = resolve_scale(scale);
+  args.B = int(batch); args.Hq = num_q_heads; args.Hk = num_k_heads; args.Hv = num_v_heads;
+  return device_status(gdn::launch_decode(args, static_cast<hipStream_t>(stream), variant),
+                       "gdn_decode_pooled launch");
+}
+
 int prefill_impl(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v, const float* state, const float* A_log,
                  const gdn_bf16* a, const float* dt_bias, const gdn_bf16* b, const void* cu_seqlens,
                  int32_t cu_seqlens_dtype, int64_t num_seqs, int64_t total_tokens, double scale, gdn_bf16* output,
@@ -207,9 +208,32 @@ int prefill_impl(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v, const 
   return device_status(gdn::launch_prefill(args, static_cast<hipStream_t>(stream)), "gdn_prefill launch");
 }
 
+int check_variant(int32_t variant) {
+  if (variant < 0 || variant >= gdn::kDecodeVariants)
+    return fail(GDN_ERR_INVALID_ARGUMENT, "variant must be in [0, %d) (got %d)", gdn::kDecodeVariants, variant);
+  return ok();
+}
+
 }  // namespace
 
 extern "C" {
+
+int gdn_decode(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v, const float* state,
+               const float* A_log, const gdn_bf16* a, const float* dt_bias, const gdn_bf16* b, double scale,
+               gdn_bf16* output, float* new_state, int64_t batch, int32_t num_q_heads, int32_t num_k_heads,
+               int32_t num_v_heads, int32_t head_dim_k, int32_t head_dim_v, void* stream) {
+  return decode_impl(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state, batch, num_q_heads,
+                     num_k_heads, num_v_heads, head_dim_k, head_dim_v, -1, stream);
+}
+
+int gdn_decode_pooled(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v, float* state_pool,
+                      int64_t pool_slots, const int32_t* state_indices, const float* A_log, const gdn_bf16* a,
+                      const float* dt_bias, const gdn_bf16* b, double scale, gdn_bf16* output, int64_t batch,
+                      int32_t num_q_heads, int32_t num_k_heads, int32_t num_v_heads, int32_t head_dim_k,
+                      int32_t head_dim_v, void* stream) {
+  return decode_pooled_impl(q, k, v, state_pool, pool_slots, state_indices, A_log, a, dt_bias, b, scale, output,
+                            batch, num_q_heads, num_k_heads, num_v_heads, head_dim_k, head_dim_v, -1, stream);
+}
 
 int gdn_prefill(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v, const float* state, const float* A_log,
                 const gdn_bf16* a, const float* dt_bias, const gdn_bf16* b, const void* cu_seqlens,
@@ -219,6 +243,29 @@ int gdn_prefill(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v, const f
   return prefill_impl(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu_seqlens_dtype, num_seqs, total_tokens,
                       scale, output, new_state, num_q_heads, num_k_heads, num_v_heads, head_dim_k, head_dim_v, 0, 0,
                       nullptr, stream);
+}
+
+int gdn_decode_num_variants(void) { return gdn::kDecodeVariants; }
+
+int gdn_decode_with_variant(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v, const float* state,
+                            const float* A_log, const gdn_bf16* a, const float* dt_bias, const gdn_bf16* b,
+                            double scale, gdn_bf16* output, float* new_state, int64_t batch, int32_t num_q_heads,
+                            int32_t num_k_heads, int32_t num_v_heads, int32_t head_dim_k, int32_t head_dim_v,
+                            int32_t variant, void* stream) {
+  GDN_TRY(check_variant(variant));
+  return decode_impl(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state, batch, num_q_heads,
+                     num_k_heads, num_v_heads, head_dim_k, head_dim_v, variant, stream);
+}
+
+int gdn_decode_pooled_with_variant(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v, float* state_pool,
+                                   int64_t pool_slots, const int32_t* state_indices, const float* A_log,
+                                   const gdn_bf16* a, const float* dt_bias, const gdn_bf16* b, double scale,
+                                   gdn_bf16* output, int64_t batch, int32_t num_q_heads, int32_t num_k_heads,
+                                   int32_t num_v_heads, int32_t head_dim_k, int32_t head_dim_v, int32_t variant,
+                                   void* stream) {
+  GDN_TRY(check_variant(variant));
+  return decode_pooled_impl(q, k, v, state_pool, pool_slots, state_indices, A_log, a, dt_bias, b, scale, output,
+                            batch, num_q_heads, num_k_heads, num_v_heads, head_dim_k, head_dim_v, variant, stream);
 }
 
 int gdn_prefill_fault_injection(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v, const float* state,

@@ -21,8 +21,6 @@
 #include "gdn_common.hpp"
 #include "gdn_launch.hpp"
 
-#include <stdlib.h>
-
 namespace gdn {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
@@ -133,25 +131,14 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_decode_kernel(DecodeArgs p) {
 
 namespace {
 
-// Launch shapes (rows per wave, waves per workgroup, nontemporal state access).
-// GDN_DECODE_VARIANT=<i> (read once) overrides the size heuristic.
+// Launch shapes (rows per wave, waves per workgroup, nontemporal state access),
+// numbered as the variant argument of launch_decode.
 #define GDN_DECODE_VARIANTS(X)                                                              \
   X(0, 16, 4, true) X(1, 8, 4, true) X(2, 4, 4, true) X(3, 2, 4, true) X(4, 8, 2, true)    \
   X(5, 4, 2, true) X(6, 16, 2, true) X(7, 32, 4, true) X(8, 8, 1, true) X(9, 4, 1, true)   \
   X(10, 16, 4, false) X(11, 8, 4, false) X(12, 4, 4, false) X(13, 2, 2, true)              \
   X(14, 16, 1, true) X(15, 2, 1, true)
-
-constexpr int kNumVariants = 16;
-
-int forced_variant() {
-  static const int v = [] {
-    const char* e = getenv("GDN_DECODE_VARIANT");
-    if (!e) return -1;
-    const int i = atoi(e);
-    return (i >= 0 && i < kNumVariants) ? i : -1;
-  }();
-  return v;
-}
+static_assert(kDecodeVariants == 16, "the variant table has 16 entries");
 
 template <int RPW, int WAVES, bool NT>
 hipError_t launch_variant(const DecodeArgs& a, hipStream_t stream) {
@@ -170,9 +157,9 @@ hipError_t launch_variant(const DecodeArgs& a, hipStream_t stream) {
 
 }  // namespace
 
-hipError_t launch_decode(const DecodeArgs& a, hipStream_t stream) {
-  int vi = forced_variant();
-  if (vi < 0) {
+hipError_t launch_decode(const DecodeArgs& a, hipStream_t stream, int variant) {
+  int vi = variant;
+  if (vi < 0 || vi >= kDecodeVariants) {
     const int64_t heads = int64_t(a.B) * a.Hv;
     // Measured on MI355X (B=64 and pooled B=512, cold cache): 8 rows per wave,
     // 4 waves, nontemporal state traffic is fastest; small batches use one-wave

@@ -46,7 +46,10 @@ struct PrefillArgs {
   unsigned* aborts;         // non-null: +1 (device atomic) each time a wait gives up
 };
 
-hipError_t launch_decode(const DecodeArgs& args, hipStream_t stream);
+// Decode launch shapes (rows per wave x waves per workgroup x nontemporal state
+// access), numbered 0 .. kDecodeVariants-1; variant < 0 picks by batch size.
+constexpr int kDecodeVariants = 16;
+hipError_t launch_decode(const DecodeArgs& args, hipStream_t stream, int variant = -1);
 hipError_t launch_prefill(const PrefillArgs& args, hipStream_t stream);
 
 }  // namespace gdn

@@ -148,6 +148,19 @@ def test_prefill_fault_injection_rejects(lib, kw, code, frag):
         assert "spin_limit" in _lib.last_error()
 
 
+def test_decode_variant_entry_points_validate(lib):
+    """The launch-shape testing entry points reject out-of-range shapes (and whatever
+    gdn_decode rejects) before any device call."""
+    n = lib.gdn_decode_num_variants()
+    assert n == 16
+    for bad in (-1, n):
+        assert lib.gdn_decode_with_variant(*dec_args(), bad, None) == INVALID
+        assert "variant" in _lib.last_error()
+        assert lib.gdn_decode_pooled_with_variant(*pool_args(), bad, None) == INVALID
+    assert lib.gdn_decode_with_variant(*dec_args(dk=64), 0, None) == UNSUPPORTED
+    assert lib.gdn_decode_pooled_with_variant(*pool_args(slots=0), 0, None) == INVALID
+
+
 def test_last_error_is_cleared_on_success(lib):
     lib.gdn_decode_check(*dec_args(B=-1))
     assert _lib.last_error()

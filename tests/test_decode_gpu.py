@@ -3,7 +3,7 @@ import numpy as np
 import pytest
 import torch
 
-from gdn_kernel_amd import binding, workloads
+from gdn_kernel_amd import _lib, binding, workloads
 from gdn_kernel_amd.workloads import Heads, to_numpy
 from oracle import gdn_oracle as O
 from tests.conftest import assert_close
@@ -151,3 +151,50 @@ def test_decode_golden_fixture(gpu):
     torch.cuda.synchronize()
     assert_close(host(out), fx["out_ref"], OUT_RTOL, OUT_ATOL, "output")
     assert_close(host(ns), fx["state_ref"], STATE_RTOL, STATE_ATOL, "new_state")
+
+
+def test_decode_every_launch_shape(gpu):
+    """Every compiled decode launch shape (rows per wavefront x wavefronts per workgroup
+    x nontemporal access), selected through gdn_decode_with_variant /
+    gdn_decode_pooled_with_variant, against the oracle: in place, with a null state, and
+    pooled with a padding row.  Production picks two of them by batch size."""
+    lib = _lib.load()
+    nv = lib.gdn_decode_num_variants()
+    assert nv == 16
+    stream = torch.cuda.current_stream(gpu).cuda_stream
+    ptr = lambda t: None if t is None else t.data_ptr()
+    w = workloads.decode_inputs(5, seed=31, gate="slow", state_scale=1.0)
+    wn = workloads.decode_inputs(5, seed=32, gate="baseline", with_state=False)
+    slots = 9
+    wp = workloads.decode_inputs(4, seed=33, gate="slow", pool_slots=slots, state_scale=1.0)
+    idx = wp["state_indices"].clone()
+    idx[2] = -1
+    o_ref, s_ref = oracle_decode(w)
+    on_ref, sn_ref = oracle_decode(wn)
+    op_ref, pool_ref = O.decode_pooled(*[to_numpy(wp[k]) for k in ("q", "k", "v", "state")],
+                                       idx.numpy(), *[to_numpy(wp[k]) for k in
+                                                      ("A_log", "a", "dt_bias", "b")], wp["scale"])
+    H = (16, 16, 32, 128, 128)
+    for variant in range(nv):
+        say(f"decode launch shape {variant}")
+        for ws, st_ref, ou_ref in ((w, s_ref, o_ref), (wn, sn_ref, on_ref)):
+            d = {k: (v.to(gpu) if isinstance(v, torch.Tensor) else v) for k, v in ws.items()}
+            out = torch.full_like(d["v"], float("nan"))
+            ns = d["state"].clone() if d["state"] is not None else \
+                torch.full((5, 32, 128, 128), float("nan"), device=gpu)
+            st = ns if d["state"] is not None else None          # in place
+            _lib.check(lib.gdn_decode_with_variant(
+                ptr(d["q"]), ptr(d["k"]), ptr(d["v"]), ptr(st), ptr(d["A_log"]), ptr(d["a"]),
+                ptr(d["dt_bias"]), ptr(d["b"]), d["scale"], ptr(out), ptr(ns), 5, *H, variant, stream))
+            torch.cuda.synchronize()
+            assert_close(host(out), ou_ref, OUT_RTOL, OUT_ATOL, f"shape {variant} output")
+            assert_close(host(ns), st_ref, STATE_RTOL, STATE_ATOL, f"shape {variant} new_state")
+        d = {k: (v.to(gpu) if isinstance(v, torch.Tensor) else v) for k, v in wp.items()}
+        pool = d["state"].clone()
+        out = torch.full_like(d["v"], float("nan"))
+        _lib.check(lib.gdn_decode_pooled_with_variant(
+            ptr(d["q"]), ptr(d["k"]), ptr(d["v"]), ptr(pool), slots, ptr(idx.to(gpu)), ptr(d["A_log"]),
+            ptr(d["a"]), ptr(d["dt_bias"]), ptr(d["b"]), d["scale"], ptr(out), 4, *H, variant, stream))
+        torch.cuda.synchronize()
+        assert_close(host(out), op_ref, OUT_RTOL, OUT_ATOL, f"shape {variant} pooled output")
+        assert_close(host(pool), pool_ref, STATE_RTOL, STATE_ATOL, f"shape {variant} pool")

@@ -310,3 +310,29 @@ def test_prefill_bounded_waits(gpu):
     o3, s3 = run_prefill(p, gpu)
     torch.cuda.synchronize()
     assert torch.equal(o3, o1) and torch.equal(s3, s1)
+
+
+@pytest.mark.parametrize("seed", range(6))
+def test_prefill_random_batches(gpu, seed):
+    """Seeded random batches against the oracle: 1-9 sequences with lengths drawn from
+    the chunk-boundary values (0, 1, 63, 64, 65, 128) and uniformly up to 300, random
+    head ratios, gate distribution and cu_seqlens dtype, with and without initial
+    states.  The batch sizes land on different launch variants (chains split 1-8 ways)."""
+    rng = np.random.default_rng(1000 + seed)
+    n = int(rng.integers(1, 10))
+    special = [0, 1, 63, 64, 65, 128]
+    lens = [int(rng.choice(special)) if rng.random() < 0.4 else int(rng.integers(1, 301)) for _ in range(n)]
+    hq, hk, hv = [(16, 16, 32), (8, 8, 32), (4, 8, 8), (2, 2, 8), (4, 4, 16)][int(rng.integers(0, 5))]
+    gate = "slow" if rng.random() < 0.5 else "baseline"
+    with_state = bool(rng.random() < 0.8)
+    cu_dtype = torch.int64 if rng.random() < 0.5 else torch.int32
+    say(f"prefill random batch seed={seed} lens={lens} heads=({hq},{hk},{hv}) gate={gate} "
+        f"state={with_state} cu={cu_dtype}")
+    p = workloads.prefill_inputs(lens, Heads(hq, hk, hv), seed=2000 + seed, gate=gate,
+                                 state_scale=0.5 if gate == "slow" else 0.05, with_state=with_state,
+                                 cu_dtype=cu_dtype)
+    o_ref, s_ref = oracle_prefill(p)
+    out, ns = run_prefill(p, gpu)
+    torch.cuda.synchronize()
+    assert_close(host(out), o_ref, OUT_RTOL, OUT_ATOL, "output")
+    assert_close(host(ns), s_ref, STATE_RTOL, STATE_ATOL, "new_state")
