@@ -60,6 +60,62 @@ def build(verbose: bool = False, out: Path | None = None) -> Path:
     return out
 
 
+# TVM-FFI exports (one `kernel` symbol per module, as the reference's two solutions):
+# host-only C++ over the C ABI, built when the tvm-ffi headers can be found.
+TVM_FFI_SHIMS = {"decode": "tvm_ffi/kernel.cpp", "prefill": "tvm_ffi/kernel_prefill.cpp"}
+
+
+def tvm_ffi_paths() -> dict | None:
+    """Include directories (and the library, if known) of an installed tvm-ffi:
+    TVM_FFI_INCLUDE / DLPACK_INCLUDE / TVM_FFI_LIB from the environment, else the
+    ``tvm_ffi`` Python package's libinfo.  None when the headers are not found."""
+    inc = os.environ.get("TVM_FFI_INCLUDE")
+    dl = os.environ.get("DLPACK_INCLUDE")
+    lib = os.environ.get("TVM_FFI_LIB")
+    if not inc:
+        try:
+            from tvm_ffi import libinfo  # type: ignore
+            inc = libinfo.find_include_path()
+            dl = dl or libinfo.find_dlpack_include_path()
+            lib = lib or libinfo.find_libtvm_ffi()
+        except Exception:  # not installed, or a layout this build does not know
+            return None
+    if not inc or not (Path(inc) / "tvm" / "ffi" / "function.h").exists():
+        return None
+    return {"include": [d for d in (inc, dl) if d], "lib": lib}
+
+
+def build_tvm_ffi(verbose: bool = False, paths: dict | None = None) -> dict:
+    """Compile the TVM-FFI shims into ``libgdn_kernel_amd_tvm_ffi_{decode,prefill}.so``
+    (linked against ``libgdn_kernel_amd.so``, which must be built).  Returns
+    {op: path}, or {} when tvm-ffi is not available."""
+    paths = paths if paths is not None else tvm_ffi_paths()
+    if paths is None:
+        if verbose:
+            print("tvm-ffi headers not found: TVM-FFI shims not built", flush=True)
+        return {}
+    cxx = os.environ.get("CXX") or shutil.which("g++") or "c++"
+    built = {}
+    for op, src in TVM_FFI_SHIMS.items():
+        out = PKG_DIR / f"libgdn_kernel_amd_tvm_ffi_{op}.so"
+        cmd = [cxx, "-O2", "-std=c++17", "-fPIC", "-shared", "-I", str(PKG_DIR.parent / "include")]
+        for d in paths["include"]:
+            cmd += ["-I", str(d)]
+        cmd += [str(CSRC / src), "-L", str(PKG_DIR), "-lgdn_kernel_amd", "-Wl,-rpath,$ORIGIN"]
+        if paths.get("lib"):
+            cmd += [str(paths["lib"])]
+        cmd += ["-o", str(out)]
+        if verbose:
+            print(" ".join(cmd), flush=True)
+        res = subprocess.run(cmd, capture_output=True, text=True)
+        if res.returncode != 0:
+            raise RuntimeError(f"TVM-FFI shim ({op}) failed to build:\n{res.stdout}{res.stderr}")
+        built[op] = out
+    return built
+
+
 if __name__ == "__main__":
     path = build(verbose="-v" in sys.argv)
     print(f"built {path}")
+    for op, p in build_tvm_ffi(verbose=True).items():
+        print(f"built {p} (TVM-FFI `kernel`, {op})")
