@@ -171,11 +171,6 @@ __device__ __forceinline__ uint2 col4_tr(const uint16_t* tile, int stride, int k
   return read_tr(tile + (k0 + 4 * g + (j >> 2)) * stride + perm(col0 + 4 * (j & 3)));
 }
 
-// The same for a tile with plain column order.
-__device__ __forceinline__ uint2 col4_tr_plain(const uint16_t* tile, int stride, int k0, int col0, int lane) {
-  const int j = lane & 15, g = lane >> 4;
-  return read_tr(tile + (k0 + 4 * g + (j >> 2)) * stride + col0 + 4 * (j & 3));
-}
 
 // Operand column of the K tile for the state update: column 16 kt + lane%16 (of
 // the unpermuted k index), contraction rows 32 ks + kappa(g, s), as two
@@ -909,21 +904,30 @@ __device__ __forceinline__ void retrieve(const ChunkBufs& cb, const f32x4 (&S)[V
   }
 }
 
+// State row (within the wave's VW rows) held by column n of state tile vt.  With two
+// tiles the rows interleave in groups of four (tile 0: 0-3, 8-11, ..., tile 1: 4-7,
+// 12-15, ...), so that a lane's output rows of the two tiles are 8 consecutive values.
+template <int VT>
+__device__ __forceinline__ int vrow(int vt, int n) {
+  return VT == 2 ? 8 * (n >> 2) + 4 * vt + (n & 3) : 16 * vt + n;
+}
+
 // The consumer loop: iteration t (>= 1) advances the state through chunk t-1
 // from the buffers of parity (t-1) & 1, once the producers have handed it over.
-// The wave's rows are row0 + VW wave + 16 vt + lane%16 (V columns VW wave + ...
-// of the staged slice).
+// Column n of state tile vt is state row row0 + VW wave + vrow(vt, n) (V column
+// VW wave + vrow(vt, n) of the staged slice).
 template <class V>
 __device__ __forceinline__ void consumer_loop(PrefillSmem& sm, const PrefillArgs& p, int64_t s0, int64_t s1,
                                               int nchunks, int h, int row0, int wave, int lane0,
                                               f32x4 (&S)[V::VT][8]) {
   constexpr int VT = V::VT, VW = V::VW;
   const int64_t vstride = int64_t(p.Hv) * D;
-  // Element offset of output row 16ct + lane%16, columns 4 (lane/16) .. +3, from
-  // the wave's (uniform) chunk base.
+  // Element offset of output row 16ct + lane%16, first column of the lane's output
+  // values (8 (lane/16) with two state tiles, 4 (lane/16) with one), from the wave's
+  // (uniform) chunk base.
   int orow[4];
 #pragma unroll
-  for (int ct = 0; ct < 4; ++ct) orow[ct] = (16 * ct + (lane0 & 15)) * int(vstride) + 4 * (lane0 >> 4);
+  for (int ct = 0; ct < 4; ++ct) orow[ct] = (16 * ct + (lane0 & 15)) * int(vstride) + (VT == 2 ? 8 : 4) * (lane0 >> 4);
   PhaseClock clk;
   clk.start();
   for (int t = 1; t <= nchunks; ++t) {
@@ -942,7 +946,7 @@ __device__ __forceinline__ void consumer_loop(PrefillSmem& sm, const PrefillArgs
     clk.lap(1);
 
     // 2: Y, v_new, output
-    // Y = beta (V - e^gamma X); element (c = 16ct + 4g + i, v = VW w + 16vt + n16).
+    // Y = beta (V - e^gamma X); element (c = 16ct + 4g + i, v = VW w + vrow(vt, n16)).
 #pragma unroll
     for (int ct = 0; ct < 4; ++ct) {
       const float4 bc = *reinterpret_cast<const float4*>(cb.bet + 16 * ct + 4 * g);
@@ -951,7 +955,9 @@ __device__ __forceinline__ void consumer_loop(PrefillSmem& sm, const PrefillArgs
 #pragma unroll
       for (int vt = 0; vt < VT; ++vt) {
         // V rows 16ct + 4g .. +3 of column VW w + 16vt + n16 (zero past the chunk end)
-        const uint2 vv = col4_tr_plain(sm.V, VSTR, 16 * ct, VW * wave + 16 * vt, lane);
+        // V rows 16ct + 4g .. +3 of column VW w + vrow(vt, n16): lane j of a 16-lane
+        // group reads the 4 columns VW w + vrow(vt, 4 (j & 3)) .. +3 of row 16ct + 4g + j/4.
+        const uint2 vv = read_tr(sm.V + (16 * ct + 4 * g + (n16 >> 2)) * VSTR + VW * wave + vrow<VT>(vt, 4 * (n16 & 3)));
         const float vf[4] = {bf16lo_f32(vv.x), bf16hi_f32(vv.x), bf16lo_f32(vv.y), bf16hi_f32(vv.y)};
 #pragma unroll
         for (int i = 0; i < 4; ++i) Xk[ct][vt][i] = b4[i] * (vf[i] - e4[i] * Xk[ct][vt][i]);
@@ -999,15 +1005,20 @@ __device__ __forceinline__ void consumer_loop(PrefillSmem& sm, const PrefillArgs
         for (int vt = 0; vt < VT; ++vt) Xq[vt][ct] = mfma(vb[vt], pq, Xq[vt][ct]);
       }
     }
-    // Lane holds o[c = 16ct + n16][v = row0 + VW w + 16vt + 4g .. +3]: one 8-byte store each.
+    // Lane holds o[c = 16ct + n16][v = row0 + VW w + vrow(vt, 4g + i)]: with two tiles
+    // that is 8 consecutive v (one 16-byte store per ct), with one 4 (8 bytes).
     uint16_t* obase = p.out + cs * vstride + (int64_t(h) * D + row0 + VW * wave);
 #pragma unroll
     for (int ct = 0; ct < 4; ++ct) {
       if (16 * ct + n16 < clen) {
-#pragma unroll
-        for (int vt = 0; vt < VT; ++vt) {
-          const f32x4& o = Xq[vt][ct];
-          *reinterpret_cast<uint2*>(obase + orow[ct] + 16 * vt) = uint2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
+        if constexpr (VT == 2) {
+          const f32x4 &o0 = Xq[0][ct], &o1 = Xq[1][ct];
+          *reinterpret_cast<uint4*>(obase + orow[ct]) =
+              uint4{pack_bf16x2(o0[0], o0[1]), pack_bf16x2(o0[2], o0[3]), pack_bf16x2(o1[0], o1[1]),
+                    pack_bf16x2(o1[2], o1[3])};
+        } else {
+          const f32x4& o = Xq[0][ct];
+          *reinterpret_cast<uint2*>(obase + orow[ct]) = uint2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
         }
       }
     }
@@ -1129,13 +1140,13 @@ __global__ __launch_bounds__(V::NTHREADS) void gdn_prefill_kernel(PrefillArgs p)
     return;
   }
 
-  // Consumer state slab: rows v = row0 + VW*wave + 16*vt + n16, cols k = 16*kt + 4g + i.
+  // Consumer state slab: rows v = row0 + VW*wave + vrow(vt, n16), cols k = 16*kt + 4g + i.
   const int64_t state_head = (int64_t(seq) * p.Hv + h) * D * D;
   const int g = lane0 >> 4, n16 = lane0 & 15;
   f32x4 S[VT][8];
 #pragma unroll
   for (int vt = 0; vt < VT; ++vt) {
-    const int v = row0 + VW * wave + 16 * vt + n16;
+    const int v = row0 + VW * wave + vrow<VT>(vt, n16);
 #pragma unroll
     for (int kt = 0; kt < 8; ++kt) {
       if (p.state) {
@@ -1152,7 +1163,7 @@ __global__ __launch_bounds__(V::NTHREADS) void gdn_prefill_kernel(PrefillArgs p)
   if (nchunks > 0 || p.state != p.new_state) {
 #pragma unroll
     for (int vt = 0; vt < VT; ++vt) {
-      const int v = row0 + VW * wave + 16 * vt + n16;
+      const int v = row0 + VW * wave + vrow<VT>(vt, n16);
 #pragma unroll
       for (int kt = 0; kt < 8; ++kt) {
         const f32x4 x = S[vt][kt];
