@@ -36,6 +36,9 @@ SIGNATURES = {
                     c_int),
     "gdn_prefill_check": ([_P] * 8 + [_P, c_int32, c_int64, c_int64, c_double, _P, _P] + _HEADS,
                           c_int),
+    "gdn_prefill_workspace_size": ([c_int64, c_int64, c_int32], c_int64),
+    "gdn_prefill_with_workspace": ([_P] * 8 + [_P, c_int32, c_int64, c_int64, c_double, _P, _P]
+                                   + _HEADS + [_P, c_int64, _P], c_int),
     # include/gdn_kernel_amd_testing.h
     "gdn_decode_num_variants": ([], c_int),
     "gdn_decode_with_variant": ([_P] * 8 + [c_double, _P, _P, c_int64] + _HEADS + [c_int32, _P], c_int),

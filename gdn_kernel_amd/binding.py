@@ -170,7 +170,8 @@ def prefill_kernel(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, outp
     q,k [T,H{q,k},128] bf16 (a leading batch dim of 1 is accepted); v [T,Hv,128]
     bf16; state [N,Hv,128,128] fp32 or None; a,b [T,Hv] bf16; cu_seqlens [N+1]
     int32 or int64 on the device; output [T,Hv,128] bf16; new_state
-    [N,Hv,128,128] fp32 (may be ``state``)."""
+    [N,Hv,128,128] fp32 (may be ``state``).  Batches of few (sequence, head)
+    chains take a workspace from torch's caching allocator (gdn_prefill_with_workspace)."""
     dev = _device_of(q)
 
     def squeeze1(t, name, nd):
@@ -209,8 +210,13 @@ def prefill_kernel(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, outp
     _need(new_state, "new_state", _F32, (N, Hv, dv, dk), dev)
     lib = _lib.load()
     with _on_device(dev):
-        rc = lib.gdn_prefill(_ptr(q), _ptr(k), _ptr(v), _ptr(state), _ptr(A_log), _ptr(a),
-                             _ptr(dt_bias), _ptr(b), cu_seqlens.data_ptr(), cu_code, N, T,
-                             _scale(scale), _ptr(output), _ptr(new_state), Hq, Hk, Hv, dk, dv,
-                             _stream(dev))
+        # Batches of few (sequence, head) chains prepare their chunks in a first
+        # kernel; its workspace comes from torch's caching allocator on this stream.
+        ws_bytes = lib.gdn_prefill_workspace_size(N, T, Hv)
+        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes > 0 else None
+        rc = lib.gdn_prefill_with_workspace(_ptr(q), _ptr(k), _ptr(v), _ptr(state), _ptr(A_log),
+                                            _ptr(a), _ptr(dt_bias), _ptr(b), cu_seqlens.data_ptr(),
+                                            cu_code, N, T, _scale(scale), _ptr(output),
+                                            _ptr(new_state), Hq, Hk, Hv, dk, dv, _ptr(ws), ws_bytes,
+                                            _stream(dev))
     _lib.check(rc)

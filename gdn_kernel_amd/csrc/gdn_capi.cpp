@@ -188,12 +188,25 @@ int prefill_impl(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v, const 
                  int32_t cu_seqlens_dtype, int64_t num_seqs, int64_t total_tokens, double scale, gdn_bf16* output,
                  float* new_state, int32_t num_q_heads, int32_t num_k_heads, int32_t num_v_heads,
                  int32_t head_dim_k, int32_t head_dim_v, int32_t spin_limit, int32_t ready_chunks,
-                 uint32_t* aborts, void* stream) {
+                 uint32_t* aborts, void* workspace, int64_t workspace_bytes, void* stream) {
   GDN_TRY(gdn_prefill_check(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu_seqlens_dtype, num_seqs,
                             total_tokens, scale, output, new_state, num_q_heads, num_k_heads, num_v_heads,
                             head_dim_k, head_dim_v));
+  uint16_t* tiles = nullptr;
+  if (workspace != nullptr) {
+    const int64_t need = gdn::prefill_workspace_bytes(int(num_seqs), total_tokens, num_v_heads);
+    if (need > 0) {
+      if (workspace_bytes < need)
+        return fail(GDN_ERR_INVALID_ARGUMENT, "workspace_bytes is %lld, this batch needs %lld",
+                    static_cast<long long>(workspace_bytes), static_cast<long long>(need));
+      if (reinterpret_cast<uintptr_t>(workspace) % 16 != 0)
+        return fail(GDN_ERR_INVALID_ARGUMENT, "workspace must be 16-byte aligned");
+      tiles = static_cast<uint16_t*>(workspace);
+    }
+  }
   if (num_seqs == 0) return ok();
   gdn::PrefillArgs args{};
+  args.tiles = tiles;
   args.spin_limit = spin_limit;
   args.ready_chunks = ready_chunks;
   args.aborts = aborts;
@@ -242,7 +255,23 @@ int gdn_prefill(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v, const f
                 int32_t head_dim_k, int32_t head_dim_v, void* stream) {
   return prefill_impl(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu_seqlens_dtype, num_seqs, total_tokens,
                       scale, output, new_state, num_q_heads, num_k_heads, num_v_heads, head_dim_k, head_dim_v, 0, 0,
-                      nullptr, stream);
+                      nullptr, nullptr, 0, stream);
+}
+
+int64_t gdn_prefill_workspace_size(int64_t num_seqs, int64_t total_tokens, int32_t num_v_heads) {
+  if (num_seqs <= 0 || num_seqs > INT32_MAX || total_tokens <= 0 || num_v_heads <= 0) return 0;
+  return gdn::prefill_workspace_bytes(int(num_seqs), total_tokens, num_v_heads);
+}
+
+int gdn_prefill_with_workspace(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v, const float* state,
+                               const float* A_log, const gdn_bf16* a, const float* dt_bias, const gdn_bf16* b,
+                               const void* cu_seqlens, int32_t cu_seqlens_dtype, int64_t num_seqs,
+                               int64_t total_tokens, double scale, gdn_bf16* output, float* new_state,
+                               int32_t num_q_heads, int32_t num_k_heads, int32_t num_v_heads, int32_t head_dim_k,
+                               int32_t head_dim_v, void* workspace, int64_t workspace_bytes, void* stream) {
+  return prefill_impl(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu_seqlens_dtype, num_seqs, total_tokens,
+                      scale, output, new_state, num_q_heads, num_k_heads, num_v_heads, head_dim_k, head_dim_v, 0, 0,
+                      nullptr, workspace, workspace_bytes, stream);
 }
 
 int gdn_decode_num_variants(void) { return gdn::kDecodeVariants; }
@@ -280,7 +309,7 @@ int gdn_prefill_fault_injection(const gdn_bf16* q, const gdn_bf16* k, const gdn_
                 ready_chunks);
   return prefill_impl(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu_seqlens_dtype, num_seqs, total_tokens,
                       scale, output, new_state, num_q_heads, num_k_heads, num_v_heads, head_dim_k, head_dim_v,
-                      spin_limit, ready_chunks, aborts, stream);
+                      spin_limit, ready_chunks, aborts, nullptr, 0, stream);
 }
 
 }  // extern "C"

@@ -44,7 +44,16 @@ struct PrefillArgs {
   int spin_limit;           // polls before a hand-off wait gives up; 0 => the default (~70 ms)
   int ready_chunks;         // > 0: producers signal "chunk ready" only for chunks < ready_chunks
   unsigned* aborts;         // non-null: +1 (device atomic) each time a wait gives up
+  // Two-kernel path: workspace of prefill_workspace_bytes(...) bytes for the
+  // prepared T~/P tiles; null (or a batch that the single kernel serves) => one kernel.
+  uint16_t* tiles;
+  int prep_chunks;          // set by the launcher: consecutive chunks per prep workgroup
 };
+
+// Workspace bytes of the two-kernel prefill path for these sizes on the current
+// device, or 0 when the single kernel serves them (many chains, or a workspace
+// above the cap).
+int64_t prefill_workspace_bytes(int N, int64_t T, int Hv);
 
 // Decode launch shapes (rows per wave x waves per workgroup x nontemporal state
 // access), numbered 0 .. kDecodeVariants-1; variant < 0 picks by batch size.

@@ -65,6 +65,7 @@ namespace {
 typedef __bf16 bf16x8_t __attribute__((ext_vector_type(8)));
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef short i16x4 __attribute__((ext_vector_type(4)));
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 typedef __attribute__((address_space(3))) i16x4 lds_i16x4;
 
 constexpr int C = 64;        // chunk length
@@ -75,9 +76,11 @@ constexpr int TSTR = 72;     // bf16 row stride of 64-wide tiles (T~, P, N)
 constexpr int NDB = 16 * 16 + 4;  // floats per diagonal N block (column-major; padded by 16 bytes)
 constexpr int NROWS = C - 16;  // rows of N kept for the off-diagonal solve
 
-template <int NCW_, int VT_, bool HOOKS_ = false>
+template <int NCW_, int VT_, bool HOOKS_ = false, bool LOAD_ = false>
 struct Variant {
   static constexpr bool kHooks = HOOKS_;         // testing hooks of PrefillArgs compiled in
+  static constexpr bool kLoad = LOAD_;           // waves NCW.. load prepared T~/P (two-kernel path)
+  static constexpr bool kCopy = false;           // producers copy their tiles out (prep kernel only)
   static constexpr int NCW = NCW_;               // consumer waves
   static constexpr int VT = VT_;                 // 16-row state tiles per consumer wave
   static constexpr int VW = 16 * VT;             // state rows per consumer wave
@@ -87,9 +90,25 @@ struct Variant {
   static constexpr int VSEG = 8 * ROWS;          // 16-byte segments of the V slice of a chunk
   static_assert(F * ROWS == 128 && NCW + 4 <= 8, "unsupported launch variant");
 };
+
+// The prep kernel of the two-kernel path: the four producer waves alone (no
+// consumers, no V staging); they copy each chunk's tiles out themselves (kCopy).
+struct PrepVariant {
+  static constexpr bool kHooks = false, kLoad = false, kCopy = true;
+  static constexpr int NCW = 0, VT = 1, VW = 16, ROWS = 128, F = 1;
+  static constexpr int NTHREADS = 64 * (NCW + 4);
+  static constexpr int VSEG = 0;
+};
+
+// Prepared tiles of one chunk-head in the workspace: the LDS images of T~ hi,
+// T~ lo and P, in that order (strictly-upper blocks zero), in 16-byte units.
+// Chunk t of sequence s, v-head h is image (s TC + t) Hv + h, TC = ceil(T / C)
+// (a sequence clamped into [0, T] has at most TC chunks).
+constexpr int kTileImage = 3 * C * TSTR / 8;
 constexpr int kMaxSortedSeqs = 1024;  // longest-first ordering up to this many sequences
 
 struct __align__(16) PrefillSmem {
+  static constexpr int kParities = 2;  // chunk buffers in flight
   uint16_t K[2][C * KSTR];    // K chunk [c][perm(k)], by chunk parity
   uint16_t Q[2][C * KSTR];    // Q chunk [c][perm(k)]
   uint16_t Th[2][C * TSTR];   // T~ hi [c][perm(j)] (strictly-upper blocks stay 0)
@@ -107,6 +126,29 @@ struct __align__(16) PrefillSmem {
   int sync[8];                // hand-off counters (kReady, kVFree, kConsumed, kPPhase, kAbort, kDiagN, kX32)
   int spin_limit;             // kernels with testing hooks: polls before a hand-off wait gives up
   unsigned* aborts;           // kernels with testing hooks: optional count of waits that gave up
+};
+
+// LDS of the prep kernel (two-kernel path): one chunk's buffers (the producers
+// stage chunk t + 1 once the copier has written chunk t out) and no V, so that two
+// workgroups share a CU.
+struct __align__(16) PrepSmem {
+  static constexpr int kParities = 1;
+  uint16_t K[1][C * KSTR];
+  uint16_t Q[1][C * KSTR];
+  uint16_t Th[1][C * TSTR];
+  uint16_t Tl[1][C * TSTR];
+  uint16_t P[1][C * TSTR];
+  uint16_t V[8];              // no V is staged (PrepVariant::VSEG = 0)
+  uint16_t Nh[NROWS * TSTR];
+  uint16_t Nl[NROWS * TSTR];
+  float Nd[4 * NDB];
+  float gam[1][C];
+  float bet[1][C];
+  float eg[1][C];
+  float dd[1][C];
+  int sync[8];
+  int spin_limit;
+  unsigned* aborts;
 };
 
 constexpr float kLog2e = 1.4426950408889634f;
@@ -302,7 +344,8 @@ __device__ __forceinline__ void wave_lds_sync() {
 enum SyncCounter { kReady = 0, kVFree = 1, kConsumed = 2, kPPhase = 3, kAbort = 4, kDiagN = 5, kX32 = 6 };
 constexpr int kSpinLimit = 1 << 21;  // default polls (about 70 ms) before a wait gives up
 
-__device__ __forceinline__ void signal_count(PrefillSmem& sm, int which, int lane) {
+template <class Smem>
+__device__ __forceinline__ void signal_count(Smem& sm, int which, int lane) {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
   if (lane == 0) __hip_atomic_fetch_add(&sm.sync[which], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
 }
@@ -313,8 +356,8 @@ __device__ __forceinline__ void signal_count(PrefillSmem& sm, int which, int lan
 // workgroup still finishes (with wrong results) instead of hanging.  Production
 // kernels give up after kSpinLimit polls; kernels built with the hooks after
 // sm.spin_limit polls, counting each give-up in sm.aborts if set.
-template <bool kHooks>
-__device__ __forceinline__ void wait_count(PrefillSmem& sm, int which, int target) {
+template <bool kHooks, class Smem>
+__device__ __forceinline__ void wait_count(Smem& sm, int which, int target) {
   if (__hip_atomic_load(&sm.sync[which], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < target) {
     for (int it = 0;; ++it) {
       __builtin_amdgcn_s_sleep(1);
@@ -388,7 +431,9 @@ struct ChunkBufs {
   float* dd;
 };
 
-__device__ __forceinline__ ChunkBufs chunk_bufs(PrefillSmem& sm, int b) {
+template <class Smem>
+__device__ __forceinline__ ChunkBufs chunk_bufs(Smem& sm, int b) {
+  b %= Smem::kParities;
   return ChunkBufs{sm.K[b], sm.Q[b], sm.Th[b], sm.Tl[b], sm.P[b], sm.gam[b], sm.bet[b], sm.eg[b], sm.dd[b]};
 }
 
@@ -411,7 +456,8 @@ __device__ __forceinline__ f32x4 ld4(const float* p) {
 
 // Branch-free epilogues: gamma is non-increasing along the chunk, so every
 // exponent kept is <= 0; the masked ones are clamped to 0 before the select.
-__device__ __forceinline__ void tile_epilogue(PrefillSmem& sm, const ChunkBufs& cb, const TileJob t, const f32x4& acc,
+template <class Smem>
+__device__ __forceinline__ void tile_epilogue(Smem& sm, const ChunkBufs& cb, const TileJob t, const f32x4& acc,
                                               float scale, int lane) {
   const int g = lane >> 4, n16 = lane & 15;
   if (t.kind == 1) {
@@ -444,8 +490,8 @@ __device__ __forceinline__ void tile_epilogue(PrefillSmem& sm, const ChunkBufs& 
   }
 }
 
-template <int NJ>
-__device__ __forceinline__ void run_tiles(PrefillSmem& sm, const ChunkBufs& cb, const TileJob (&jobs)[NJ], float scale,
+template <int NJ, class Smem>
+__device__ __forceinline__ void run_tiles(Smem& sm, const ChunkBufs& cb, const TileJob (&jobs)[NJ], float scale,
                                           int lane) {
   f32x4 acc[NJ];
 #pragma unroll
@@ -478,8 +524,8 @@ __device__ __forceinline__ void run_tiles(PrefillSmem& sm, const ChunkBufs& cb, 
 //   x_m = delta_mj - a_m,  a_i += N[i][m] x_m  for i > m
 // (for m < j every term is zero, so x_m = 0 there).  The column of N needed at
 // step m is one broadcast read per four rows; no cross-lane traffic.
-template <int I0, int I1>
-__device__ __forceinline__ void diag_tiles(PrefillSmem& sm, const ChunkBufs& cb, int lane) {
+template <int I0, int I1, class Smem>
+__device__ __forceinline__ void diag_tiles(Smem& sm, const ChunkBufs& cb, int lane) {
   const int g = lane >> 4, n16 = lane & 15;
   {
     f32x4 acc[4];
@@ -506,7 +552,8 @@ __device__ __forceinline__ void diag_tiles(PrefillSmem& sm, const ChunkBufs& cb,
   }
 }
 
-__device__ __forceinline__ void diag_solve(PrefillSmem& sm, const ChunkBufs& cb, int lane) {
+template <class Smem>
+__device__ __forceinline__ void diag_solve(Smem& sm, const ChunkBufs& cb, int lane) {
   const int r = lane >> 4, j = lane & 15;
   const float* nb = sm.Nd + r * NDB;
   // Columns are read kColAhead steps ahead of their use.
@@ -612,7 +659,8 @@ __device__ __forceinline__ f32x4 finish_block(const ChunkBufs& cb, const f32x4& 
 // X20 and X30 (offdiag_left); the left wave reads X32 back from T~ once the
 // right wave has stored it (counter kX32).  Each wave reads all of its LDS
 // operands before its first block store.
-__device__ __forceinline__ void offdiag_right(PrefillSmem& sm, const ChunkBufs& cb, int t, int lane) {
+template <class Smem>
+__device__ __forceinline__ void offdiag_right(Smem& sm, const ChunkBufs& cb, int t, int lane) {
   const Pair2 d1 = diag_b(cb, 1, lane), d2 = diag_b(cb, 2, lane);
   const Pair2 a2 = block_a(cb.Th, cb.Tl, 0, 2, 2, lane), a3 = block_a(cb.Th, cb.Tl, 0, 3, 3, lane);
   const Pair2 n21 = block_a(sm.Nh, sm.Nl, 16, 2, 1, lane), n31 = block_a(sm.Nh, sm.Nl, 16, 3, 1, lane),
@@ -629,8 +677,8 @@ __device__ __forceinline__ void offdiag_right(PrefillSmem& sm, const ChunkBufs& 
   (void)t;
 }
 
-template <bool kHooks>
-__device__ __forceinline__ void offdiag_left(PrefillSmem& sm, const ChunkBufs& cb, int t, int lane) {
+template <bool kHooks, class Smem>
+__device__ __forceinline__ void offdiag_left(Smem& sm, const ChunkBufs& cb, int t, int lane) {
   const Pair2 d0 = diag_b(cb, 0, lane);
   const Pair2 a1 = block_a(cb.Th, cb.Tl, 0, 1, 1, lane), a2 = block_a(cb.Th, cb.Tl, 0, 2, 2, lane),
               a3 = block_a(cb.Th, cb.Tl, 0, 3, 3, lane);
@@ -694,15 +742,56 @@ __device__ __forceinline__ void producer_prefetch(const PrefillArgs& p, int64_t 
   }
 }
 
+// Step 1 of a chunk: the prefetched K and Q rows into the chunk's tiles
+// (permuted columns) and, on the first wave, the chunk's gates.
+__device__ __forceinline__ void stage_kq_gates(const ChunkBufs& cb, const ProducerPrefetch& f, int pt, int pw, int lane,
+                                               int clen, float neg_decay, float dt_bias) {
+#pragma unroll
+  for (int it = 0; it < 4; ++it) {
+    const int c = (pt >> 4) + 16 * it, sg = pt & 15;
+    const int col0 = (8 * sg) & ~31, r0 = (8 * sg) & 31;
+    const int pa = kq_off(c, col0 + perm32(r0)), pb = kq_off(c, col0 + perm32(r0 + 4));
+    *reinterpret_cast<uint2*>(cb.K + pa) = uint2{f.k[it].x, f.k[it].y};
+    *reinterpret_cast<uint2*>(cb.K + pb) = uint2{f.k[it].z, f.k[it].w};
+    *reinterpret_cast<uint2*>(cb.Q + pa) = uint2{f.q[it].x, f.q[it].y};
+    *reinterpret_cast<uint2*>(cb.Q + pb) = uint2{f.q[it].z, f.q[it].w};
+  }
+  if (pw == 0) {
+    const float lg = lane < clen ? fast_log_gate(neg_decay, bf16_to_f32(f.a) + dt_bias) : 0.f;
+    const float bt = lane < clen ? fast_sigmoid(bf16_to_f32(f.b)) : 0.f;
+    const float gm = wave_inclusive_scan(lg);
+    const float glast = readlane_f(gm, clen - 1);
+    cb.gam[lane] = gm;
+    cb.bet[lane] = bt;
+    cb.eg[lane] = exp_le0(gm);
+    cb.dd[lane] = exp_le0(glast - gm);
+  }
+}
+
 // The producer loop: chunk t is prepared into the buffers of parity t & 1 once
 // the consumers are done with chunk t - 2 (same parity).  The four producer waves
 // meet twice per chunk (after staging; after the tiles and diagonal blocks) on
 // their own counter; the chunk is handed over when all four are done.  V is
 // staged for the workgroup's state rows [row0, row0 + ROWS) only.
-template <class V>
-__device__ __forceinline__ void producer_loop(PrefillSmem& sm, const PrefillArgs& p, int64_t s0, int64_t s1,
-                                              int nchunks, int h, int hq, int hk, int row0, int pw, int lane0) {
-  constexpr int NVIT = (V::VSEG + NPROD - 1) / NPROD;  // V segments per producer thread
+// Producer thread pt's share of a chunk's T~ hi, T~ lo and P tiles (their LDS
+// images) to the chunk's image in the workspace.
+__device__ __forceinline__ void copy_tiles_out(const ChunkBufs& cb, u32x4* image, int pt) {
+  constexpr int NT1 = C * TSTR / 8;
+  for (int e = pt; e < kTileImage; e += NPROD) {
+    const uint16_t* src = e < NT1 ? cb.Th + 8 * e : e < 2 * NT1 ? cb.Tl + 8 * (e - NT1) : cb.P + 8 * (e - 2 * NT1);
+    image[e] = *reinterpret_cast<const u32x4*>(src);
+  }
+}
+
+// With V::kCopy (the prep kernel, no consumers) the producers also write each
+// chunk's tiles to images (chunk t of the run at images + t Hv kTileImage): chunk
+// t - 1's at the start of tick t, once all four waves have handed it over, and
+// before the staging barrier, after which tick t writes the same buffers.
+template <class V, class Smem>
+__device__ __forceinline__ void producer_loop(Smem& sm, const PrefillArgs& p, int64_t s0, int64_t s1,
+                                              int nchunks, int h, int hq, int hk, int row0, int pw, int lane0,
+                                              u32x4* images = nullptr) {
+  constexpr int NVIT = V::VSEG > 0 ? (V::VSEG + NPROD - 1) / NPROD : 1;  // V segments per producer thread
   const int pt = pw * 64 + lane0;
   const float neg_decay = -expf(p.A_log[h]);
   const float dt_bias = p.dt_bias[h];
@@ -731,30 +820,19 @@ __device__ __forceinline__ void producer_loop(PrefillSmem& sm, const PrefillArgs
     const int64_t ncs = cs + C;
     const int nclen = int(s1 - ncs < C ? s1 - ncs : C);
     const ChunkBufs cb = chunk_bufs(sm, t & 1);
-    if (t >= 2) wait_count<V::kHooks>(sm, kConsumed, V::NCW * (t - 1));  // chunk t - 2 consumed
+    // The buffers of chunk t - kParities (the same ones) consumed.
+    constexpr int kPar = Smem::kParities;
+    if (t >= kPar) wait_count<V::kHooks>(sm, kConsumed, V::NCW * (t - kPar + 1));
+    if constexpr (V::kCopy) {
+      if (t >= 1) {
+        wait_count<V::kHooks>(sm, kReady, 4 * t);  // chunk t - 1 handed over by all four waves
+        copy_tiles_out(chunk_bufs(sm, (t - 1) & 1), images + int64_t(t - 1) * p.Hv * kTileImage, pt);
+      }
+    }
     clk.lap(0);
 
     // 1: stage K/Q (permuted columns), gates
-#pragma unroll
-    for (int it = 0; it < 4; ++it) {
-      const int c = (pt >> 4) + 16 * it, sg = pt & 15;
-      const int col0 = (8 * sg) & ~31, r0 = (8 * sg) & 31;
-      const int pa = kq_off(c, col0 + perm32(r0)), pb = kq_off(c, col0 + perm32(r0 + 4));
-      *reinterpret_cast<uint2*>(cb.K + pa) = uint2{f.k[it].x, f.k[it].y};
-      *reinterpret_cast<uint2*>(cb.K + pb) = uint2{f.k[it].z, f.k[it].w};
-      *reinterpret_cast<uint2*>(cb.Q + pa) = uint2{f.q[it].x, f.q[it].y};
-      *reinterpret_cast<uint2*>(cb.Q + pb) = uint2{f.q[it].z, f.q[it].w};
-    }
-    if (pw == 0) {
-      const float lg = lane < clen ? fast_log_gate(neg_decay, bf16_to_f32(f.a) + dt_bias) : 0.f;
-      const float bt = lane < clen ? fast_sigmoid(bf16_to_f32(f.b)) : 0.f;
-      const float gm = wave_inclusive_scan(lg);
-      const float glast = readlane_f(gm, clen - 1);
-      cb.gam[lane] = gm;
-      cb.bet[lane] = bt;
-      cb.eg[lane] = exp_le0(gm);
-      cb.dd[lane] = exp_le0(glast - gm);
-    }
+    stage_kq_gates(cb, f, pt, pw, lane, clen, neg_decay, dt_bias);
     // The V slice of this chunk into registers; staged at the end of the tick,
     // after the consumers' last read of the previous chunk's V.
     {
@@ -867,6 +945,106 @@ __device__ __forceinline__ void producer_loop(PrefillSmem& sm, const PrefillArgs
     }
     __builtin_amdgcn_s_setprio(0);
     if (!V::kHooks || p.ready_chunks <= 0 || t < p.ready_chunks) signal_count(sm, kReady, lane);
+    clk.lap(9);
+  }
+  if constexpr (V::kCopy) {
+    wait_count<V::kHooks>(sm, kReady, 4 * nchunks);
+    copy_tiles_out(chunk_bufs(sm, (nchunks - 1) & 1), images + int64_t(nchunks - 1) * p.Hv * kTileImage, pt);
+  }
+  clk.store(V::NCW + pw, lane0);
+}
+
+// The loader loop of the two-kernel path: the producers' hand-offs and staging,
+// with chunk t's T~ (hi, lo) and P copied from their prepared images (tiles =
+// image of chunk 0 of this chain; chunk t is Hv images further) instead of
+// computed.  K, Q and the gates are staged as the producers stage them, V at the
+// end of the tick, after the consumers' last read of the previous chunk's V.
+// The images and V of chunk t + 1 are loaded into registers during tick t, so
+// their latency overlaps the waits for the consumers.
+template <class V>
+__device__ __forceinline__ void loader_loop(PrefillSmem& sm, const PrefillArgs& p, const u32x4* tiles, int64_t s0,
+                                            int64_t s1, int nchunks, int h, int hq, int hk, int row0, int pw,
+                                            int lane0) {
+  constexpr int NVIT = (V::VSEG + NPROD - 1) / NPROD;        // V segments per loader thread
+  constexpr int NTIT = (kTileImage + NPROD - 1) / NPROD;     // 16-byte tile units per loader thread
+  constexpr int NT1 = C * TSTR / 8;                          // 16-byte units per tile
+  const int pt = pw * 64 + lane0;
+  const float neg_decay = -expf(p.A_log[h]);
+  const float dt_bias = p.dt_bias[h];
+  const LaneOffsets lo = {(pt >> 4) * p.Hk * D + 8 * (pt & 15), (pt >> 4) * p.Hq * D + 8 * (pt & 15), pt * p.Hv};
+  int voff[NVIT], vrow[NVIT];
+#pragma unroll
+  for (int it = 0; it < NVIT; ++it) {
+    const int seg = pt + it * NPROD, c = seg / (V::ROWS / 8), sg = seg % (V::ROWS / 8);
+    vrow[it] = seg < V::VSEG ? c : C;  // C: no segment
+    voff[it] = c * p.Hv * D + 8 * sg;
+  }
+  // Unit pt + 256 it of a chunk's images (the last round's excess lanes re-read
+  // the last unit and store nothing).
+  int toff[NTIT];
+#pragma unroll
+  for (int it = 0; it < NTIT; ++it) toff[it] = pt + it * NPROD < kTileImage ? pt + it * NPROD : kTileImage - 1;
+  // (First-class vectors: copies of uint4 structs would go through the stack.)
+  u32x4 tv[NTIT], fv[NVIT];
+  ProducerPrefetch f;
+  producer_prefetch(p, s0, int(s1 - s0 < C ? s1 - s0 : C), h, hq, hk, pt, lo, f);
+  // Chunk 0's images and V slice into registers.
+#pragma unroll
+  for (int it = 0; it < NTIT; ++it) tv[it] = tiles[toff[it]];
+  {
+    const int clen0 = int(s1 - s0 < C ? s1 - s0 : C);
+    const uint16_t* vb = p.v + (s0 * p.Hv + h) * D + row0;
+#pragma unroll
+    for (int it = 0; it < NVIT; ++it) {
+      fv[it] = u32x4{0u, 0u, 0u, 0u};
+      if (vrow[it] < clen0) fv[it] = *reinterpret_cast<const u32x4*>(vb + voff[it]);
+    }
+  }
+  PhaseClock clk;
+  clk.start();
+
+  for (int t = 0; t < nchunks; ++t) {
+    int lane = lane0;
+    asm volatile("" : "+v"(lane));
+    const int64_t cs = s0 + int64_t(t) * C;
+    const int clen = int(s1 - cs < C ? s1 - cs : C);
+    const int64_t ncs = cs + C;
+    const int nclen = int(s1 - ncs < C ? s1 - ncs : C);
+    const ChunkBufs cb = chunk_bufs(sm, t & 1);
+    if (t >= 2) wait_count<V::kHooks>(sm, kConsumed, V::NCW * (t - 1));  // chunk t - 2 consumed
+    clk.lap(0);
+    stage_kq_gates(cb, f, pt, pw, lane, clen, neg_decay, dt_bias);
+    if (ncs < s1) producer_prefetch(p, ncs, nclen, h, hq, hk, pt, lo, f);
+    clk.lap(1);
+#pragma unroll
+    for (int it = 0; it < NTIT; ++it) {
+      const int e = pt + it * NPROD;
+      if (e < kTileImage) {
+        uint16_t* dst = e < NT1 ? cb.Th + 8 * e : e < 2 * NT1 ? cb.Tl + 8 * (e - NT1) : cb.P + 8 * (e - 2 * NT1);
+        *reinterpret_cast<u32x4*>(dst) = tv[it];
+      }
+    }
+    clk.lap(7);
+    if (t >= 1) wait_count<V::kHooks>(sm, kVFree, V::NCW * t);  // the consumers' last read of V
+    clk.lap(8);
+#pragma unroll
+    for (int it = 0; it < NVIT; ++it) {
+      const int seg = pt + it * NPROD;
+      if (seg < V::VSEG)
+        *reinterpret_cast<u32x4*>(sm.V + (seg / (V::ROWS / 8)) * VSTR + 8 * (seg % (V::ROWS / 8))) = fv[it];
+    }
+    signal_count(sm, kReady, lane);
+    if (t + 1 < nchunks) {  // chunk t + 1's images and V slice into registers
+      const u32x4* src = tiles + int64_t(t + 1) * p.Hv * kTileImage;
+#pragma unroll
+      for (int it = 0; it < NTIT; ++it) tv[it] = src[toff[it]];
+      const uint16_t* vb = p.v + (ncs * p.Hv + h) * D + row0;
+#pragma unroll
+      for (int it = 0; it < NVIT; ++it) {
+        fv[it] = u32x4{0u, 0u, 0u, 0u};
+        if (vrow[it] < nclen) fv[it] = *reinterpret_cast<const u32x4*>(vb + voff[it]);
+      }
+    }
     clk.lap(9);
   }
   clk.store(V::NCW + pw, lane0);
@@ -1136,7 +1314,15 @@ __global__ __launch_bounds__(V::NTHREADS) void gdn_prefill_kernel(PrefillArgs p)
   __syncthreads();  // cleared LDS and counters visible to both roles
 
   if (wave >= NCW) {
-    if (nchunks > 0) producer_loop<V>(sm, p, s0, s1, nchunks, h, hq, hk, row0, wave - NCW, lane0);
+    if (nchunks > 0) {
+      if constexpr (V::kLoad) {
+        const int64_t tc = (p.T + C - 1) / C;
+        const u32x4* tiles = reinterpret_cast<const u32x4*>(p.tiles) + (int64_t(seq) * tc * p.Hv + h) * kTileImage;
+        loader_loop<V>(sm, p, tiles, s0, s1, nchunks, h, hq, hk, row0, wave - NCW, lane0);
+      } else {
+        producer_loop<V>(sm, p, s0, s1, nchunks, h, hq, hk, row0, wave - NCW, lane0);
+      }
+    }
     return;
   }
 
@@ -1174,6 +1360,55 @@ __global__ __launch_bounds__(V::NTHREADS) void gdn_prefill_kernel(PrefillArgs p)
   }
 }
 
+// Prep kernel of the two-kernel path (few chains).  Workgroup b = (s R' + r) Hv + h
+// prepares chunks r p.prep_chunks .. (r + 1) p.prep_chunks - 1 of sequence s for
+// v-head h (R' = ceil(TC / p.prep_chunks)): the producer waves run their loop over
+// those chunks and copy each one's T~ hi, T~ lo and P tiles (LDS images) to its
+// image in p.tiles; their loads of chunk t + 1 are in flight meanwhile.  Its LDS
+// (PrepSmem, one chunk's buffers, no V) lets two workgroups share a CU.  Chunks are
+// independent, so all of them are prepared at once; the state pass (Variant<..,
+// LOAD = true>) then only copies them.
+__global__ __launch_bounds__(PrepVariant::NTHREADS) void gdn_prefill_prep_kernel(PrefillArgs p) {
+  constexpr int NTHREADS = PrepVariant::NTHREADS;
+  __shared__ PrepSmem sm;
+  const int tid = threadIdx.x;
+  const int lane0 = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int64_t tc = (p.T + C - 1) / C;
+  const int run = p.prep_chunks;
+  const int64_t runs = (tc + run - 1) / run;
+  const int64_t bid = blockIdx.x;
+  const int h = int(bid % p.Hv);
+  const int seq = int(bid / p.Hv / runs), r = int(bid / p.Hv % runs);
+  int64_t s0 = load_cu(p.cu_seqlens, p.cu_is_64, seq);
+  int64_t s1 = load_cu(p.cu_seqlens, p.cu_is_64, seq + 1);
+  s0 = s0 < 0 ? 0 : (s0 > p.T ? p.T : s0);
+  s1 = s1 < s0 ? s0 : (s1 > p.T ? p.T : s1);
+  const int64_t t0 = int64_t(r) * run;           // first chunk of the run
+  const int64_t cs = s0 + t0 * C;
+  if (cs >= s1) return;  // the sequence has no chunk t0 (workgroup-uniform)
+  const int64_t ce = s1 - cs < int64_t(run) * C ? s1 : cs + int64_t(run) * C;
+  const int nchunks = int((ce - cs + C - 1) / C);
+  const int hq = h / (p.Hv / p.Hq);
+  const int hk = h / (p.Hv / p.Hk);
+
+  // Blocks never written per chunk are zeros (as in the one-kernel path).
+  const uint4 z = uint4{0u, 0u, 0u, 0u};
+  for (int e = tid; e < C * TSTR / 8; e += NTHREADS) {
+    reinterpret_cast<uint4*>(sm.P[0])[e] = z;
+    reinterpret_cast<uint4*>(sm.Th[0])[e] = z;
+    reinterpret_cast<uint4*>(sm.Tl[0])[e] = z;
+    if (e < NROWS * TSTR / 8) {
+      reinterpret_cast<uint4*>(sm.Nh)[e] = z;
+      reinterpret_cast<uint4*>(sm.Nl)[e] = z;
+    }
+  }
+  if (tid < 8) sm.sync[tid] = 0;
+  __syncthreads();
+  u32x4* images = reinterpret_cast<u32x4*>(p.tiles) + ((int64_t(seq) * tc + t0) * p.Hv + h) * kTileImage;
+  producer_loop<PrepVariant>(sm, p, cs, ce, nchunks, h, hq, hk, 0, wave, lane0, images);
+}
+
 template <class V>
 hipError_t launch_variant(const PrefillArgs& a, hipStream_t stream) {
   const int64_t chains = int64_t(a.N) * a.Hv;
@@ -1201,13 +1436,34 @@ int device_cus() {
 #define GDN_PREFILL_MAX_SPLIT 8
 #endif
 
+namespace {
 // Chains are split F ways (F a power of two, at most GDN_PREFILL_MAX_SPLIT)
 // while the split grid still fits one workgroup per CU.
-hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream) {
-  const int64_t chains = int64_t(a.N) * a.Hv;
+int split_factor(int64_t chains) {
   const int64_t cus = device_cus();
   int F = 1;
   while (F < GDN_PREFILL_MAX_SPLIT && chains * 2 * F <= cus) F *= 2;
+  return F;
+}
+
+// Largest workspace the two-kernel path uses; bigger batches take one kernel.
+constexpr int64_t kMaxWorkspaceBytes = int64_t(2) << 30;
+}  // namespace
+
+// Batches split 8 ways repeat the producer work in every slice of a chain and are
+// bound by it (the 16-row consumer is faster); the two-kernel path prepares each
+// chunk once, all chunks in parallel, so that the state pass runs at the
+// consumer's pace.  Fewer slices (32-row consumers) gain nothing from it.
+int64_t prefill_workspace_bytes(int N, int64_t T, int Hv) {
+  if (N <= 0 || Hv <= 0 || T <= 0 || split_factor(int64_t(N) * Hv) != 8) return 0;
+  const int64_t images = int64_t(N) * ((T + C - 1) / C) * Hv;
+  if (images > INT32_MAX) return 0;
+  const int64_t bytes = images * kTileImage * 16;
+  return bytes <= kMaxWorkspaceBytes ? bytes : 0;
+}
+
+hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream) {
+  const int F = split_factor(int64_t(a.N) * a.Hv);
   // Launches that use the testing hooks get kernels with the hooks compiled in;
   // production launches keep them out of the device code.
   if (a.spin_limit != 0 || a.ready_chunks != 0 || a.aborts != nullptr) {
@@ -1217,6 +1473,21 @@ hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream) {
       case 4: return launch_variant<Variant<1, 2, true>>(a, stream);
       default: return launch_variant<Variant<1, 1, true>>(a, stream);
     }
+  }
+  if (a.tiles != nullptr && prefill_workspace_bytes(a.N, a.T, a.Hv) > 0) {
+    // Runs of consecutive chunks per prep workgroup, about two workgroups per CU
+    // for the batch's chunks (at most T / C + N of them).
+    const int64_t tc = (a.T + C - 1) / C;
+    const int64_t chunks = a.T / C + a.N < a.N * tc ? a.T / C + a.N : a.N * tc;
+    const int64_t slots = 2 * int64_t(device_cus());
+    const int64_t run = (chunks * a.Hv + slots - 1) / slots;
+    PrefillArgs b = a;
+    b.prep_chunks = int(run < 1 ? 1 : run > tc ? tc : run);
+    const int64_t grid = int64_t(a.N) * ((tc + b.prep_chunks - 1) / b.prep_chunks) * a.Hv;
+    hipLaunchKernelGGL(gdn_prefill_prep_kernel, dim3(unsigned(grid)), dim3(PrepVariant::NTHREADS), 0, stream, b);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+    return launch_variant<Variant<1, 1, false, true>>(a, stream);
   }
   switch (F) {
     case 1: return launch_variant<Variant<4, 2>>(a, stream);

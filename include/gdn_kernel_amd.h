@@ -130,6 +130,36 @@ int gdn_prefill_check(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v,
                       int32_t num_q_heads, int32_t num_k_heads, int32_t num_v_heads,
                       int32_t head_dim_k, int32_t head_dim_v);
 
+/*
+ * Prefill with a caller-owned device workspace.  No reference counterpart (the
+ * reference allocates nothing and has no workspace argument); the Python
+ * `kernel` binding uses it.  Batches of very few (sequence, head) chains (at
+ * most 32 on a 256-CU device) are split 8 ways across workgroups, each of which
+ * would repeat the chunk preparation (T~ and P).  With a workspace, the
+ * preparation runs once per chunk in a first kernel, for all chunks in
+ * parallel, and the state pass only copies it.
+ *   gdn_prefill_workspace_size: bytes this path needs for num_seqs sequences,
+ *     total_tokens tokens and num_v_heads v-heads on the current device;
+ *     0 when gdn_prefill serves the batch with one kernel anyway (more chains,
+ *     or more than 2 GiB of workspace).  Touches no device memory.
+ *   gdn_prefill_with_workspace: gdn_prefill's arguments plus the workspace
+ *     (16-byte aligned, at least the size above, and not shared with a launch
+ *     that may run concurrently).  A NULL workspace, or a batch whose size is 0,
+ *     runs gdn_prefill.  The results equal gdn_prefill's bit for bit (the same
+ *     code prepares the chunks).
+ */
+int64_t gdn_prefill_workspace_size(int64_t num_seqs, int64_t total_tokens,
+                                   int32_t num_v_heads);
+
+int gdn_prefill_with_workspace(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v,
+                               const float* state, const float* A_log, const gdn_bf16* a,
+                               const float* dt_bias, const gdn_bf16* b, const void* cu_seqlens,
+                               int32_t cu_seqlens_dtype, int64_t num_seqs, int64_t total_tokens,
+                               double scale, gdn_bf16* output, float* new_state,
+                               int32_t num_q_heads, int32_t num_k_heads, int32_t num_v_heads,
+                               int32_t head_dim_k, int32_t head_dim_v, void* workspace,
+                               int64_t workspace_bytes, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -148,6 +148,36 @@ def test_prefill_fault_injection_rejects(lib, kw, code, frag):
         assert "spin_limit" in _lib.last_error()
 
 
+def test_prefill_workspace_size(lib):
+    """Bytes of the two-kernel prefill path: N ceil(T / 64) Hv chunk images of 27,648
+    bytes (T~ hi, T~ lo and P, 64 x 72 bf16 each) for batches whose chains are split 8
+    ways across workgroups (at most 32 chains on 256 CUs), 0 otherwise.  Without a GPU
+    the CU count defaults to 256."""
+    assert lib.gdn_prefill_workspace_size(1, 4096, 32) == 64 * 32 * 27648
+    assert lib.gdn_prefill_workspace_size(3, 100, 8) == 3 * 2 * 8 * 27648
+    assert lib.gdn_prefill_workspace_size(2, 4096, 16) == 2 * 64 * 16 * 27648    # 32 chains
+    assert lib.gdn_prefill_workspace_size(2, 4096, 32) == 0                      # 64 chains: one kernel
+    assert lib.gdn_prefill_workspace_size(5, 4096, 32) == 0
+    for n, t, hv in ((0, 100, 8), (1, 0, 8), (1, 100, 0), (-1, 100, 8), (1, -5, 8)):
+        assert lib.gdn_prefill_workspace_size(n, t, hv) == 0
+    assert lib.gdn_prefill_workspace_size(1, 1 << 24, 32) == 0                   # above the 2 GiB cap
+
+
+def test_prefill_with_workspace_validates(lib):
+    """gdn_prefill_with_workspace validates like gdn_prefill, then rejects a workspace
+    below the reported size or not 16-byte aligned; every case fails before any device
+    call."""
+    small = pre_args(N=1, T=4096)
+    need = lib.gdn_prefill_workspace_size(1, 4096, 32)
+    assert lib.gdn_prefill_with_workspace(*pre_args(N=-1), FAKE, need, None) == INVALID
+    assert "num_seqs" in _lib.last_error()
+    assert lib.gdn_prefill_with_workspace(*pre_args(dk=96), FAKE, need, None) == UNSUPPORTED
+    assert lib.gdn_prefill_with_workspace(*small, FAKE, need - 1, None) == INVALID
+    assert "workspace_bytes" in _lib.last_error()
+    assert lib.gdn_prefill_with_workspace(*small, FAKE + 8, need, None) == INVALID
+    assert "aligned" in _lib.last_error()
+
+
 def test_decode_variant_entry_points_validate(lib):
     """The launch-shape testing entry points reject out-of-range shapes (and whatever
     gdn_decode rejects) before any device call."""

@@ -48,10 +48,12 @@ def test_decode_graph_replays_match_eager(gpu):
         assert torch.isfinite(x)
 
 
-def test_prefill_graph_replays_match_eager(gpu):
-    say("prefill graph replay")
-    p = workloads.prefill_inputs([130, 3, 0, 64], seed=32, device=gpu, gate="slow",
-                                 state_scale=0.5)
+@pytest.mark.parametrize("lens", [[130, 3, 0, 64], [300]])
+def test_prefill_graph_replays_match_eager(gpu, lens):
+    """128 chains (one kernel) and 32 chains (two kernels: the Python kernel takes the
+    workspace from torch's allocator, which during capture is the graph's own pool)."""
+    say(f"prefill graph replay lens={lens}")
+    p = workloads.prefill_inputs(lens, seed=32, device=gpu, gate="slow", state_scale=0.5)
     T, N = p["q"].shape[0], len(p["lengths"])
     out = torch.empty((T, 32, 128), dtype=torch.bfloat16, device=gpu)
     ns = torch.empty((N, 32, 128, 128), dtype=torch.float32, device=gpu)

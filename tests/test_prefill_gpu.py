@@ -283,6 +283,57 @@ def _prefill_fault_injection(p, gpu, spin_limit, ready_chunks):
     return out, ns, aborts
 
 
+def _prefill_capi(p, gpu, workspace):
+    """gdn_prefill, or gdn_prefill_with_workspace with a workspace of exactly the
+    reported size, through the C ABI; returns (output, new_state)."""
+    d = {k: (v.to(gpu) if isinstance(v, torch.Tensor) else v) for k, v in p.items()}
+    T, Hq = d["q"].shape[0], d["q"].shape[1]
+    Hk, Hv = d["k"].shape[1], d["v"].shape[1]
+    cu = d["cu_seqlens"]
+    N = cu.numel() - 1
+    out = torch.full((T, Hv, 128), float("nan"), device=gpu, dtype=torch.bfloat16)
+    ns = torch.full((N, Hv, 128, 128), float("nan"), device=gpu, dtype=torch.float32)
+    cu_code = _lib.GDN_INDEX_INT32 if cu.dtype == torch.int32 else _lib.GDN_INDEX_INT64
+    ptr = lambda t: None if t is None else t.data_ptr()
+    args = [ptr(d["q"]), ptr(d["k"]), ptr(d["v"]), ptr(d["state"]), ptr(d["A_log"]), ptr(d["a"]),
+            ptr(d["dt_bias"]), ptr(d["b"]), cu.data_ptr(), cu_code, N, T, d["scale"], ptr(out),
+            ptr(ns), Hq, Hk, Hv, 128, 128]
+    lib = _lib.load()
+    stream = torch.cuda.current_stream(gpu).cuda_stream
+    if workspace:
+        nbytes = lib.gdn_prefill_workspace_size(N, T, Hv)
+        assert nbytes > 0, "expected a batch that the two-kernel path serves"
+        ws = torch.full((nbytes,), 0xFF, device=gpu, dtype=torch.uint8)
+        rc = lib.gdn_prefill_with_workspace(*args, ws.data_ptr(), nbytes, stream)
+    else:
+        rc = lib.gdn_prefill(*args, stream)
+    _lib.check(rc)
+    torch.cuda.synchronize()
+    return out, ns
+
+
+@pytest.mark.parametrize("lens,heads", [
+    ([300], Heads(16, 16, 32)),                  # 32 chains, each split over 8 workgroups
+    ([150, 64, 7, 0], Heads(4, 4, 8)),           # ragged, an empty sequence
+    ([1, 2, 63, 64, 129], Heads(2, 2, 4)),       # boundary lengths (chunk runs of 1 in the prep)
+    ([700, 1300], Heads(8, 8, 16)),              # runs of several chunks per prep workgroup
+])
+def test_prefill_two_kernel_path(gpu, lens, heads):
+    """Batches of at most 32 chains with a workspace: a first kernel prepares every
+    chunk's T~ and P (all chunks at once) and the state pass copies them instead of
+    recomputing them in each of a chain's 8 slices.  The preparation is the same code, so the results equal
+    gdn_prefill's bit for bit; both match the oracle.  The workspace starts as 0xFF
+    bytes, so a chunk image that the first kernel did not write would show."""
+    say(f"prefill two-kernel path lens={lens} heads={heads}")
+    p = workloads.prefill_inputs(lens, heads, seed=22, gate="slow", state_scale=0.5)
+    o1, s1 = _prefill_capi(p, gpu, workspace=False)
+    o2, s2 = _prefill_capi(p, gpu, workspace=True)
+    assert torch.equal(o1, o2) and torch.equal(s1, s2), "workspace path differs from gdn_prefill"
+    o_ref, s_ref = oracle_prefill(p)
+    assert_close(host(o2), o_ref, OUT_RTOL, OUT_ATOL, "output")
+    assert_close(host(s2), s_ref, STATE_RTOL, STATE_ATOL, "new_state")
+
+
 def test_prefill_bounded_waits(gpu):
     """The hand-off failure path, forced from the host.  With the testing hooks off
     the entry point is gdn_prefill bit for bit.  With the producers signalling only
