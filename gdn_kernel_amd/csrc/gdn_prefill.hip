@@ -1450,12 +1450,14 @@ int split_factor(int64_t chains) {
 constexpr int64_t kMaxWorkspaceBytes = int64_t(2) << 30;
 }  // namespace
 
-// Batches split 8 ways repeat the producer work in every slice of a chain and are
-// bound by it (the 16-row consumer is faster); the two-kernel path prepares each
-// chunk once, all chunks in parallel, so that the state pass runs at the
-// consumer's pace.  Fewer slices (32-row consumers) gain nothing from it.
+// Batches split 4 or 8 ways repeat the producer work in every slice of a chain and
+// are bound by it; the two-kernel path prepares each chunk once, all chunks in
+// parallel, and its state pass (no producer code: 16-row consumers fit in the
+// registers) runs at the consumers' pace.  Batches split 2 ways lose more to the
+// extra pass than they gain, and unsplit ones keep producers and consumers busy
+// on the same CUs.
 int64_t prefill_workspace_bytes(int N, int64_t T, int Hv) {
-  if (N <= 0 || Hv <= 0 || T <= 0 || split_factor(int64_t(N) * Hv) != 8) return 0;
+  if (N <= 0 || Hv <= 0 || T <= 0 || split_factor(int64_t(N) * Hv) < 4) return 0;
   const int64_t images = int64_t(N) * ((T + C - 1) / C) * Hv;
   if (images > INT32_MAX) return 0;
   const int64_t bytes = images * kTileImage * 16;
@@ -1487,6 +1489,7 @@ hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream) {
     hipLaunchKernelGGL(gdn_prefill_prep_kernel, dim3(unsigned(grid)), dim3(PrepVariant::NTHREADS), 0, stream, b);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
+    if (F == 4) return launch_variant<Variant<2, 1, false, true>>(a, stream);
     return launch_variant<Variant<1, 1, false, true>>(a, stream);
   }
   switch (F) {

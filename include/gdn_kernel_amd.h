@@ -133,8 +133,8 @@ int gdn_prefill_check(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v,
 /*
  * Prefill with a caller-owned device workspace.  No reference counterpart (the
  * reference allocates nothing and has no workspace argument); the Python
- * `kernel` binding uses it.  Batches of very few (sequence, head) chains (at
- * most 32 on a 256-CU device) are split 8 ways across workgroups, each of which
+ * `kernel` binding uses it.  Batches of few (sequence, head) chains (at most 64
+ * on a 256-CU device) are split 4 or 8 ways across workgroups, each of which
  * would repeat the chunk preparation (T~ and P).  With a workspace, the
  * preparation runs once per chunk in a first kernel, for all chunks in
  * parallel, and the state pass only copies it.

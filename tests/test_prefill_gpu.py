@@ -315,13 +315,15 @@ def _prefill_capi(p, gpu, workspace):
 @pytest.mark.parametrize("lens,heads", [
     ([300], Heads(16, 16, 32)),                  # 32 chains, each split over 8 workgroups
     ([150, 64, 7, 0], Heads(4, 4, 8)),           # ragged, an empty sequence
+    ([150, 64, 7, 0, 65, 200], Heads(4, 4, 8)),  # 48 chains: split 4 ways (two 16-row consumers)
+    ([130, 2100], Heads(16, 16, 32)),            # 64 chains, split 4 ways
     ([1, 2, 63, 64, 129], Heads(2, 2, 4)),       # boundary lengths (chunk runs of 1 in the prep)
     ([700, 1300], Heads(8, 8, 16)),              # runs of several chunks per prep workgroup
 ])
 def test_prefill_two_kernel_path(gpu, lens, heads):
-    """Batches of at most 32 chains with a workspace: a first kernel prepares every
+    """Batches of at most 64 chains with a workspace: a first kernel prepares every
     chunk's T~ and P (all chunks at once) and the state pass copies them instead of
-    recomputing them in each of a chain's 8 slices.  The preparation is the same code, so the results equal
+    recomputing them in each of a chain's 4 or 8 slices.  The preparation is the same code, so the results equal
     gdn_prefill's bit for bit; both match the oracle.  The workspace starts as 0xFF
     bytes, so a chunk image that the first kernel did not write would show."""
     say(f"prefill two-kernel path lens={lens} heads={heads}")
