@@ -1471,8 +1471,8 @@ hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream) {
   if (a.spin_limit != 0 || a.ready_chunks != 0 || a.aborts != nullptr) {
     switch (F) {
       case 1: return launch_variant<Variant<4, 2, true>>(a, stream);
-      case 2: return launch_variant<Variant<2, 2, true>>(a, stream);
-      case 4: return launch_variant<Variant<1, 2, true>>(a, stream);
+      case 2: return launch_variant<Variant<4, 1, true>>(a, stream);
+      case 4: return launch_variant<Variant<2, 1, true>>(a, stream);
       default: return launch_variant<Variant<1, 1, true>>(a, stream);
     }
   }
@@ -1492,10 +1492,13 @@ hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream) {
     if (F == 4) return launch_variant<Variant<2, 1, false, true>>(a, stream);
     return launch_variant<Variant<1, 1, false, true>>(a, stream);
   }
+  // Split chains use 16-row consumer waves (VT = 1), whose per-chunk chain is
+  // shorter than a 32-row wave's.  Unsplit chains (F = 1) keep four 32-row waves:
+  // eight 16-row waves and the four producers would exceed the register file.
   switch (F) {
     case 1: return launch_variant<Variant<4, 2>>(a, stream);
-    case 2: return launch_variant<Variant<2, 2>>(a, stream);
-    case 4: return launch_variant<Variant<1, 2>>(a, stream);
+    case 2: return launch_variant<Variant<4, 1>>(a, stream);
+    case 4: return launch_variant<Variant<2, 1>>(a, stream);
     default: return launch_variant<Variant<1, 1>>(a, stream);
   }
 }
