@@ -1271,7 +1271,13 @@ __global__ __launch_bounds__(V::NTHREADS) void gdn_prefill_kernel(PrefillArgs p)
 
   const int tid = threadIdx.x;
   const int lane0 = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int hw = __builtin_amdgcn_readfirstlane(tid >> 6);
+  // Role index.  Waves are dealt to the four SIMDs round-robin.  In the loader
+  // variant with one consumer, the consumer takes hardware wave 3, a SIMD to itself,
+  // and two (mostly idle) loaders share SIMD 0: config 3 174 -> 170 us.  Elsewhere
+  // the natural order measured as fast or faster (two consumers on SIMDs of their
+  // own: +1.5%; the producer variant's solve wave sharing a SIMD: +7%).
+  const int wave = !(V::kLoad && NCW == 1) ? hw : hw == 3 ? 0 : hw < 3 ? hw + 1 : hw;
 
   const int bid = blockIdx.x;
   const int chain = V::F == 1 ? bid : (bid / (8 * V::F)) * 8 + bid % 8;
