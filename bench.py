@@ -91,6 +91,50 @@ def pmc_run(torch, binding, workloads):
     torch.cuda.synchronize()
 
 
+GEMM_N = 8192   # measured bf16 GEMM peak: torch.matmul of two 8192 x 8192 bf16 matrices
+
+
+def measured_peaks(torch):
+    """What this GPU reaches on plain library work, for roofline fractions against
+    measured rather than datasheet peaks: a device-to-device copy of COPY_BYTES
+    (read + written bytes over time, 4 rotating buffer pairs so the Infinity Cache
+    does not serve it) and a bf16 GEMM through torch.matmul (hipBLASLt), both timed
+    with HIP events after untimed warm-up."""
+    dev = torch.device("cuda:0")
+    pairs = [(torch.ones(COPY_BYTES // 4, dtype=torch.float32, device=dev),
+              torch.empty(COPY_BYTES // 4, dtype=torch.float32, device=dev)) for _ in range(4)]
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    for src, dst in pairs * 2:
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    reps = 20
+    e0.record()
+    for i in range(reps):
+        src, dst = pairs[i % 4]
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize()
+    copy_gbs = 2 * COPY_BYTES * reps / (e0.elapsed_time(e1) * 1e-3) / 1e9
+    del pairs
+    g = torch.Generator(device=dev).manual_seed(0)
+    a = torch.randn((GEMM_N, GEMM_N), generator=g, dtype=torch.bfloat16, device=dev)
+    b = torch.randn((GEMM_N, GEMM_N), generator=g, dtype=torch.bfloat16, device=dev)
+    c = torch.empty((GEMM_N, GEMM_N), dtype=torch.bfloat16, device=dev)
+    t_end = time.perf_counter() + 0.3
+    while time.perf_counter() < t_end:
+        torch.matmul(a, b, out=c)
+        torch.cuda.synchronize()
+    reps = 20
+    e0.record()
+    for _ in range(reps):
+        torch.matmul(a, b, out=c)
+    e1.record()
+    torch.cuda.synchronize()
+    gemm_tfs = 2 * GEMM_N ** 3 * reps / (e0.elapsed_time(e1) * 1e-3) / 1e12
+    return {"copy_gbs": round(copy_gbs, 1), "copy_bytes": 2 * COPY_BYTES,
+            "bf16_gemm_tflops": round(gemm_tfs, 1), "gemm_shape": [GEMM_N, GEMM_N, GEMM_N]}
+
+
 def timed_launches(fn, steps, warmup, torch, use_graph=False):
     """Warm up, then time exactly ``steps`` launches of ``fn(i)``.
 
@@ -327,6 +371,15 @@ def main():
             res["value"] = round(res["prefill_varlen_32k"]["tokens_per_s"], 1)
             res["unit"] = "tokens/s"
             res["ms_per_step"] = round(res["prefill_varlen_32k"]["us"] / 1e3, 5)
+    # Roofline fractions against what this box measures on library work, beside the
+    # datasheet fractions above.
+    peaks = measured_peaks(torch)
+    res["measured_peaks"] = peaks
+    if "roofline" in res:
+        res["roofline"]["frac_of_measured_copy"] = round(res["roofline"]["achieved"] / peaks["copy_gbs"], 4)
+    for key in ("prefill_varlen_32k", "prefill_t4096"):
+        if key in res:
+            res[key]["frac_of_measured_gemm"] = round(res[key]["tflops"] / peaks["bf16_gemm_tflops"], 4)
     if not args.no_cpu:
         res["cpu_baseline"] = cpu_baseline(args.cpu_seconds, workloads)
         if args.only in ("prefill", "all"):
