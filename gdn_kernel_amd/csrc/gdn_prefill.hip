@@ -19,7 +19,10 @@
 // each owning rows [R0, R0 + ROWS).  They all prepare the same chunk data (the
 // producer work does not depend on the state) and each stages only its slice of
 // V.  Batches with many chains use F = 1 (four consumer waves of 32 rows); few
-// chains are split so that every CU gets a workgroup.
+// chains are split so that every CU gets a workgroup.  When the caller provides
+// a workspace, batches split 4 or 8 ways run in two kernels instead: a prep kernel
+// prepares every chunk once (all chunks in parallel), and the state pass's loader
+// waves copy its T~/P tiles where the producers would have computed them.
 //
 // Per chunk (positions >= clen are zero-padded: K = Q = V = 0, beta = 0 and
 // log-gate 0, as kernel_prefill.cu:102-114, 125-132 pads them):
@@ -768,11 +771,6 @@ __device__ __forceinline__ void stage_kq_gates(const ChunkBufs& cb, const Produc
   }
 }
 
-// The producer loop: chunk t is prepared into the buffers of parity t & 1 once
-// the consumers are done with chunk t - 2 (same parity).  The four producer waves
-// meet twice per chunk (after staging; after the tiles and diagonal blocks) on
-// their own counter; the chunk is handed over when all four are done.  V is
-// staged for the workgroup's state rows [row0, row0 + ROWS) only.
 // Producer thread pt's share of a chunk's T~ hi, T~ lo and P tiles (their LDS
 // images) to the chunk's image in the workspace.
 __device__ __forceinline__ void copy_tiles_out(const ChunkBufs& cb, u32x4* image, int pt) {
@@ -783,6 +781,12 @@ __device__ __forceinline__ void copy_tiles_out(const ChunkBufs& cb, u32x4* image
   }
 }
 
+// The producer loop: chunk t is prepared into the buffers of parity t & 1 (of
+// Smem::kParities) once the consumers are done with the chunk that used them last
+// (chunk t - 2 with two parities).  The four producer waves meet twice per chunk
+// (after staging; after the tiles and diagonal blocks) on their own counter; the
+// chunk is handed over when all four are done.  V is staged for the workgroup's
+// state rows [row0, row0 + ROWS) only.
 // With V::kCopy (the prep kernel, no consumers) the producers also write each
 // chunk's tiles to images (chunk t of the run at images + t Hv kTileImage): chunk
 // t - 1's at the start of tick t, once all four waves have handed it over, and
