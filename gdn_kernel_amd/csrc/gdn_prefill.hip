@@ -857,7 +857,8 @@ __device__ __forceinline__ void producer_loop(Smem& sm, const PrefillArgs& p, in
 
     // 2: the next chunk's K/Q loads; diagonal N tiles (the solve waits for
     // them); then the diagonal blocks of T~ (wave 0) or the off-diagonal N tiles
-    // and one P tile each (the others).
+    // and two P tiles each (the others, in the solve's shadow: P does not depend
+    // on T~).
     // Split variants (few chains, a light consumer) put the solve first: the
     // other waves issue their loads after their diagonal tile, the solve wave
     // after its solve.
@@ -880,7 +881,7 @@ __device__ __forceinline__ void producer_loop(Smem& sm, const PrefillArgs& p, in
         if (kSolveFirst && ncs < s1) producer_prefetch(p, ncs, nclen, h, hq, hk, pt, lo, f);
         const TileJob j1[2] = {{1, 1, 0}, {1, 2, 0}};
         run_tiles(sm, cb, j1, p.scale, lane);
-        const TileJob j2[1] = {{2, 0, 0}};
+        const TileJob j2[2] = {{2, 0, 0}, {2, 3, 3}};
         run_tiles(sm, cb, j2, p.scale, lane);
         break;
       }
@@ -890,7 +891,7 @@ __device__ __forceinline__ void producer_loop(Smem& sm, const PrefillArgs& p, in
         if (kSolveFirst && ncs < s1) producer_prefetch(p, ncs, nclen, h, hq, hk, pt, lo, f);
         const TileJob j1[2] = {{1, 3, 0}, {1, 2, 1}};
         run_tiles(sm, cb, j1, p.scale, lane);
-        const TileJob j2[1] = {{2, 1, 0}};
+        const TileJob j2[2] = {{2, 1, 0}, {2, 3, 0}};
         run_tiles(sm, cb, j2, p.scale, lane);
         break;
       }
@@ -900,7 +901,7 @@ __device__ __forceinline__ void producer_loop(Smem& sm, const PrefillArgs& p, in
         if (kSolveFirst && ncs < s1) producer_prefetch(p, ncs, nclen, h, hq, hk, pt, lo, f);
         const TileJob j1[2] = {{1, 3, 1}, {1, 3, 2}};
         run_tiles(sm, cb, j1, p.scale, lane);
-        const TileJob j2[1] = {{2, 1, 1}};
+        const TileJob j2[2] = {{2, 1, 1}, {2, 2, 0}};
         run_tiles(sm, cb, j2, p.scale, lane);
         break;
       }
@@ -910,28 +911,22 @@ __device__ __forceinline__ void producer_loop(Smem& sm, const PrefillArgs& p, in
     wait_count<V::kHooks>(sm, kPPhase, 4 * (2 * t + 2));  // diagonal blocks and N tiles done
     clk.lap(6);
 
-    // 3: off-diagonal blocks of T~ (waves 1 and 3), the remaining P tiles (waves
-    // 0 and 2, one on wave 1), V once the consumers have read the previous chunk's
+    // 3: off-diagonal blocks of T~ (waves 1 and 3), the remaining P tiles (two
+    // each on waves 0 and 2), V once the consumers have read the previous chunk's
     switch (pw) {
       case 0: {
         if (kSolveFirst && ncs < s1) producer_prefetch(p, ncs, nclen, h, hq, hk, pt, lo, f);
-        const TileJob j1[2] = {{2, 2, 0}, {2, 2, 1}};
+        const TileJob j1[2] = {{2, 2, 1}, {2, 2, 2}};
         run_tiles(sm, cb, j1, p.scale, lane);
-        const TileJob j2[1] = {{2, 2, 2}};
-        run_tiles(sm, cb, j2, p.scale, lane);
         break;
       }
       case 1: {
         offdiag_right(sm, cb, t, lane);
-        const TileJob j1[1] = {{2, 3, 3}};
-        run_tiles(sm, cb, j1, p.scale, lane);
         break;
       }
       case 2: {
-        const TileJob j1[2] = {{2, 3, 0}, {2, 3, 1}};
+        const TileJob j1[2] = {{2, 3, 1}, {2, 3, 2}};
         run_tiles(sm, cb, j1, p.scale, lane);
-        const TileJob j2[1] = {{2, 3, 2}};
-        run_tiles(sm, cb, j2, p.scale, lane);
         break;
       }
       default:
