@@ -51,9 +51,10 @@ def test_prefill_null_state_and_cu_dtypes(gpu, cu_dtype):
     assert not host(ns)[2].any()                      # empty sequence, zero initial state
 
 
-def test_prefill_in_place(gpu):
-    say("prefill in place")
-    p = workloads.prefill_inputs([100, 0, 20], seed=12, gate="slow", state_scale=0.5)
+@pytest.mark.parametrize("lens", [[100, 0, 20], [100, 20]])   # 96 chains: one kernel; 64: two
+def test_prefill_in_place(gpu, lens):
+    say(f"prefill in place lens={lens}")
+    p = workloads.prefill_inputs(lens, seed=12, gate="slow", state_scale=0.5)
     o1, s1 = run_prefill(p, gpu, in_place=False)
     o2, s2 = run_prefill(p, gpu, in_place=True)
     torch.cuda.synchronize()
@@ -283,9 +284,9 @@ def _prefill_fault_injection(p, gpu, spin_limit, ready_chunks):
     return out, ns, aborts
 
 
-def _prefill_capi(p, gpu, workspace):
+def _prefill_capi(p, gpu, workspace, ws=None, nbytes=None):
     """gdn_prefill, or gdn_prefill_with_workspace with a workspace of exactly the
-    reported size, through the C ABI; returns (output, new_state)."""
+    reported size (or the given buffer), through the C ABI; returns (output, new_state)."""
     d = {k: (v.to(gpu) if isinstance(v, torch.Tensor) else v) for k, v in p.items()}
     T, Hq = d["q"].shape[0], d["q"].shape[1]
     Hk, Hv = d["k"].shape[1], d["v"].shape[1]
@@ -301,9 +302,10 @@ def _prefill_capi(p, gpu, workspace):
     lib = _lib.load()
     stream = torch.cuda.current_stream(gpu).cuda_stream
     if workspace:
-        nbytes = lib.gdn_prefill_workspace_size(N, T, Hv)
-        assert nbytes > 0, "expected a batch that the two-kernel path serves"
-        ws = torch.full((nbytes,), 0xFF, device=gpu, dtype=torch.uint8)
+        if ws is None:
+            nbytes = lib.gdn_prefill_workspace_size(N, T, Hv)
+            assert nbytes > 0, "expected a batch that the two-kernel path serves"
+            ws = torch.full((nbytes,), 0xFF, device=gpu, dtype=torch.uint8)
         rc = lib.gdn_prefill_with_workspace(*args, ws.data_ptr(), nbytes, stream)
     else:
         rc = lib.gdn_prefill(*args, stream)
@@ -334,6 +336,24 @@ def test_prefill_two_kernel_path(gpu, lens, heads):
     o_ref, s_ref = oracle_prefill(p)
     assert_close(host(o2), o_ref, OUT_RTOL, OUT_ATOL, "output")
     assert_close(host(s2), s_ref, STATE_RTOL, STATE_ATOL, "new_state")
+
+
+def test_prefill_workspace_reuse(gpu):
+    """One workspace buffer, not cleared between calls, serves two different few-chain
+    batches in turn (the larger first, then a smaller one whose images overlay the
+    first's, then the larger again): every call equals gdn_prefill bit for bit, so no
+    result depends on images left by an earlier call."""
+    lib = _lib.load()
+    big = workloads.prefill_inputs([700, 300], Heads(8, 8, 16), seed=23, gate="slow", state_scale=0.5)
+    small = workloads.prefill_inputs([90, 0, 130], Heads(4, 4, 8), seed=24, gate="slow", state_scale=0.5)
+    need = [lib.gdn_prefill_workspace_size(len(p["lengths"]), p["q"].shape[0], p["v"].shape[1]) for p in (big, small)]
+    assert min(need) > 0
+    ws = torch.full((max(need),), 0x5A, device=gpu, dtype=torch.uint8)
+    for name, p, nb in (("big", big, need[0]), ("small", small, need[1]), ("big", big, need[0])):
+        say(f"prefill workspace reuse: {name} batch")
+        ref_o, ref_s = _prefill_capi(p, gpu, workspace=False)
+        o, s = _prefill_capi(p, gpu, workspace=True, ws=ws, nbytes=nb)
+        assert torch.equal(o, ref_o) and torch.equal(s, ref_s), f"{name}: workspace path differs"
 
 
 def test_prefill_bounded_waits(gpu):
