@@ -12,8 +12,10 @@ buffers (537 MB).
 Also reported on the same line: pooled decode (B=512 over a 1024-slot pool),
 chunked prefill tokens/s on the 32-sequence / 32768-token varlen batch and on
 the single 4096-token sequence (with MFMA-roofline fractions computed from the
-algorithmic 180,224 FLOP per token and v-head), and the CPU baseline (the numpy
-oracle, the reference decode definition restated, timed on the host).
+algorithmic 180,224 FLOP per token and v-head), the rates this box measures on
+library work (a device copy and a bf16 GEMM, ``measured_peaks``) with the roofline
+fractions against them, and the CPU baseline (the numpy oracle, the reference decode
+definition restated, timed on the host).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only decode|prefill]
        [--no-cpu] [--cpu-seconds S]
