@@ -26,7 +26,8 @@
 //
 // Per chunk (positions >= clen are zero-padded: K = Q = V = 0, beta = 0 and
 // log-gate 0, as kernel_prefill.cu:102-114, 125-132 pads them):
-//   gamma = inclusive cumsum of the log gates, beta = sigmoid(b)   (a1, :101-122)
+//   gamma = inclusive cumsum of the log gates, beta = sigmoid(b)   (a1, :101-122;
+//           summed in fp64 and kept as an fp32 pair, in log2 units)
 //   N[i][j] = beta_i e^{gamma_i - gamma_j} k_i.k_j   (i > j)       (:134-146, sign folded)
 //   P[i][j] = e^{gamma_i - gamma_j} q_i.k_j          (j <= i)       (:165-185; stored times scale)
 //   T~ = (I + N)^-1                                   (:148-163)
@@ -121,7 +122,8 @@ struct __align__(16) PrefillSmem {
   uint16_t Nh[NROWS * TSTR];  // N rows 16..63, hi [i - 16][perm(j)] (producers only; row block 0
   uint16_t Nl[NROWS * TSTR];  // of N is never an operand), lo
   float Nd[4 * NDB];          // diagonal 16x16 blocks of N (fp32, column-major: [block][col][row])
-  float gam[2][C];            // gamma_c (inclusive cumsum of the log gates)
+  float gam[2][C];            // gamma_c log2(e) (inclusive cumsum of the log2 gates), rounded
+  float gaml[2][C];           // its rounding error (the sum is formed in fp64)
   float bet[2][C];            // beta_c
   float eg[2][C];             // e^{gamma_c}
   float dd[2][C];             // e^{gamma_last - gamma_c}
@@ -146,6 +148,7 @@ struct __align__(16) PrepSmem {
   uint16_t Nl[NROWS * TSTR];
   float Nd[4 * NDB];
   float gam[1][C];
+  float gaml[1][C];
   float bet[1][C];
   float eg[1][C];
   float dd[1][C];
@@ -156,8 +159,9 @@ struct __align__(16) PrepSmem {
 
 constexpr float kLog2e = 1.4426950408889634f;
 
-// e^{x} for x <= 0 via the hardware exp2 (v_exp_f32).
-__device__ __forceinline__ float exp_le0(float x) { return __builtin_amdgcn_exp2f(x * kLog2e); }
+// 2^{x} for x <= 0 (the hardware exp2, v_exp_f32).  Log gates are kept in log2
+// units (gamma * log2(e)), so every decay e^{gamma_i - gamma_j} is one exp2.
+__device__ __forceinline__ float exp2_le0(float x) { return __builtin_amdgcn_exp2f(x); }
 
 __device__ __forceinline__ f32x4 mfma(const uint4& a, const uint4& b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, a),
@@ -297,28 +301,50 @@ __device__ __forceinline__ float dpp_or_zero(float x) {
   return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(x), CTRL, ROW_MASK, 0xF, true));
 }
 
-// Inclusive prefix sum over the 64 lanes of a wavefront with DPP: shifts by
-// 1, 2, 4, 8 inside each 16-lane row, then lane 15 of rows 0 / 2 into rows 1 / 3
-// (row_bcast:15) and lane 31 into rows 2 and 3 (row_bcast:31).
-__device__ __forceinline__ float wave_inclusive_scan(float x) {
-  x += dpp_or_zero<0x111, 0xF>(x);
-  x += dpp_or_zero<0x112, 0xF>(x);
-  x += dpp_or_zero<0x114, 0xF>(x);
-  x += dpp_or_zero<0x118, 0xF>(x);
-  x += dpp_or_zero<0x142, 0xA>(x);
-  x += dpp_or_zero<0x143, 0xC>(x);
-  return x;
+template <int CTRL, int ROW_MASK>
+__device__ __forceinline__ double dpp_or_zero_f64(double x) {
+  const uint64_t u = __builtin_bit_cast(uint64_t, x);
+  const uint32_t lo = __builtin_amdgcn_update_dpp(0, uint32_t(u), CTRL, ROW_MASK, 0xF, true);
+  const uint32_t hi = __builtin_amdgcn_update_dpp(0, uint32_t(u >> 32), CTRL, ROW_MASK, 0xF, true);
+  return __builtin_bit_cast(double, (uint64_t(hi) << 32) | lo);
 }
 
-constexpr float kLn2 = 0.6931471805599453f;
+// Inclusive prefix sum over the 64 lanes of a wavefront with DPP: shifts by
+// 1, 2, 4, 8 inside each 16-lane row, then lane 15 of rows 0 / 2 into rows 1 / 3
+// (row_bcast:15) and lane 31 into rows 2 and 3 (row_bcast:31).  The sum runs in
+// fp64 and is returned as a pair hi + lo of floats (lo = the rounding error of
+// hi): the decays e^{gamma_i - gamma_j} are formed from differences of these
+// sums, and with fast decay the sums reach 1e5 in magnitude while a difference
+// that matters (one that does not underflow to zero) is below 1e2 -- a plain
+// fp32 difference would carry the sums' rounding error, up to about 1e-2.
+__device__ __forceinline__ float wave_inclusive_scan2(float x, float& lo) {
+  double d = x;
+  d += dpp_or_zero_f64<0x111, 0xF>(d);
+  d += dpp_or_zero_f64<0x112, 0xF>(d);
+  d += dpp_or_zero_f64<0x114, 0xF>(d);
+  d += dpp_or_zero_f64<0x118, 0xF>(d);
+  d += dpp_or_zero_f64<0x142, 0xA>(d);
+  d += dpp_or_zero_f64<0x143, 0xC>(d);
+  const float hi = float(d);
+  lo = float(d - double(hi));
+  return hi;
+}
 
-// Log-space decay -exp(A_log) * softplus(a + dt_bias) (torch threshold 20) with
-// the hardware exp2/log2; neg_decay = -exp(A_log).  For very negative arguments
-// log(1 + e^x) loses its relative accuracy but stays within ~1e-7 absolutely.
-__device__ __forceinline__ float fast_log_gate(float neg_decay, float x) {
-  const float t = __builtin_amdgcn_exp2f(x * 1.4426950408889634f);
-  const float sp = __builtin_amdgcn_logf(1.f + t) * kLn2;
-  return neg_decay * (x > 20.f ? x : sp);
+// gamma_i - gamma_j from the pairs (hi, lo) of the compensated scan.  The hi
+// difference is exact whenever it is small against the sums (Sterbenz), so the
+// result is accurate to fp32 precision of the difference itself.
+__device__ __forceinline__ float gamma_diff(float hi_i, float lo_i, float hi_j, float lo_j) {
+  return (hi_i - hi_j) + (lo_i - lo_j);
+}
+
+// Log-space decay in log2 units, -exp(A_log) * softplus(a + dt_bias) * log2(e)
+// (torch threshold 20), with the hardware exp2/log2; neg_decay = -exp(A_log).
+// log2(1 + 2^y) is softplus(x) * log2(e) with y = x log2(e), so no conversion
+// back to natural units is needed.  For very negative arguments log2(1 + 2^y)
+// loses its relative accuracy but stays within ~2e-7 absolutely.
+__device__ __forceinline__ float fast_log2_gate(float neg_decay, float x) {
+  const float y = x * kLog2e;
+  return neg_decay * (x > 20.f ? y : __builtin_amdgcn_logf(1.f + __builtin_amdgcn_exp2f(y)));
 }
 
 __device__ __forceinline__ float fast_sigmoid(float x) {
@@ -429,6 +455,7 @@ struct ChunkBufs {
   uint16_t* Tl;
   uint16_t* P;
   float* gam;
+  float* gaml;
   float* bet;
   float* eg;
   float* dd;
@@ -437,7 +464,8 @@ struct ChunkBufs {
 template <class Smem>
 __device__ __forceinline__ ChunkBufs chunk_bufs(Smem& sm, int b) {
   b %= Smem::kParities;
-  return ChunkBufs{sm.K[b], sm.Q[b], sm.Th[b], sm.Tl[b], sm.P[b], sm.gam[b], sm.bet[b], sm.eg[b], sm.dd[b]};
+  return ChunkBufs{sm.K[b],   sm.Q[b],   sm.Th[b],  sm.Tl[b], sm.P[b],
+                   sm.gam[b], sm.gaml[b], sm.bet[b], sm.eg[b], sm.dd[b]};
 }
 
 // ---------------------------------------------------------------------------
@@ -466,11 +494,11 @@ __device__ __forceinline__ void tile_epilogue(Smem& sm, const ChunkBufs& cb, con
   if (t.kind == 1) {
     // acc[i] = k_c . k_r, c = 16J + 4g + i, r = 16I + n16  ->  N[r][c]  (r > c)
     const int r = 16 * t.I + n16;
-    const float gr = cb.gam[r], br = cb.bet[r];
-    const f32x4 gcv = ld4(cb.gam + 16 * t.J + 4 * g);
+    const float gr = cb.gam[r], grl = cb.gaml[r], br = cb.bet[r];
+    const f32x4 gcv = ld4(cb.gam + 16 * t.J + 4 * g), gcl = ld4(cb.gaml + 16 * t.J + 4 * g);
     f32x4 x;
 #pragma unroll
-    for (int i = 0; i < 4; ++i) x[i] = br * exp_le0(fminf(gr - gcv[i], 0.f)) * acc[i];
+    for (int i = 0; i < 4; ++i) x[i] = br * exp2_le0(fminf(gamma_diff(gr, grl, gcv[i], gcl[i]), 0.f)) * acc[i];
     uint2 hi, lo;
     split4(x, hi, lo);
     const int pos = (r - 16) * TSTR + perm(16 * t.J + 4 * g);
@@ -480,12 +508,12 @@ __device__ __forceinline__ void tile_epilogue(Smem& sm, const ChunkBufs& cb, con
     // acc[i] = k_j . q_c, j = 16J + 4g + i, c = 16I + n16  ->  P[c][j]  (j <= c),
     // with the output scale folded in
     const int c = 16 * t.I + n16;
-    const float gc = cb.gam[c];
-    const f32x4 gj = ld4(cb.gam + 16 * t.J + 4 * g);
+    const float gc = cb.gam[c], gcl = cb.gaml[c];
+    const f32x4 gj = ld4(cb.gam + 16 * t.J + 4 * g), gjl = ld4(cb.gaml + 16 * t.J + 4 * g);
     float pv[4];
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
-      const float x = exp_le0(fminf(gc - gj[i], 0.f)) * (acc[i] * scale);
+      const float x = exp2_le0(fminf(gamma_diff(gc, gcl, gj[i], gjl[i]), 0.f)) * (acc[i] * scale);
       pv[i] = 16 * t.J + 4 * g + i <= c ? x : 0.f;
     }
     *reinterpret_cast<uint2*>(cb.P + c * TSTR + perm(16 * t.J + 4 * g)) =
@@ -545,11 +573,12 @@ __device__ __forceinline__ void diag_tiles(Smem& sm, const ChunkBufs& cb, int la
     // (entries with r <= c are never read).
 #pragma unroll
     for (int I = I0; I < I1; ++I) {
-      const float gc = cb.gam[16 * I + n16];
-      const f32x4 gr = ld4(cb.gam + 16 * I + 4 * g), br = ld4(cb.bet + 16 * I + 4 * g);
+      const float gc = cb.gam[16 * I + n16], gcl = cb.gaml[16 * I + n16];
+      const f32x4 gr = ld4(cb.gam + 16 * I + 4 * g), grl = ld4(cb.gaml + 16 * I + 4 * g);
+      const f32x4 br = ld4(cb.bet + 16 * I + 4 * g);
       f32x4 x;
 #pragma unroll
-      for (int i = 0; i < 4; ++i) x[i] = br[i] * exp_le0(fminf(gr[i] - gc, 0.f)) * acc[I][i];
+      for (int i = 0; i < 4; ++i) x[i] = br[i] * exp2_le0(fminf(gamma_diff(gr[i], grl[i], gc, gcl), 0.f)) * acc[I][i];
       *reinterpret_cast<f32x4*>(sm.Nd + I * NDB + n16 * 16 + 4 * g) = x;
     }
   }
@@ -760,14 +789,16 @@ __device__ __forceinline__ void stage_kq_gates(const ChunkBufs& cb, const Produc
     *reinterpret_cast<uint2*>(cb.Q + pb) = uint2{f.q[it].z, f.q[it].w};
   }
   if (pw == 0) {
-    const float lg = lane < clen ? fast_log_gate(neg_decay, bf16_to_f32(f.a) + dt_bias) : 0.f;
+    const float lg = lane < clen ? fast_log2_gate(neg_decay, bf16_to_f32(f.a) + dt_bias) : 0.f;
     const float bt = lane < clen ? fast_sigmoid(bf16_to_f32(f.b)) : 0.f;
-    const float gm = wave_inclusive_scan(lg);
-    const float glast = readlane_f(gm, clen - 1);
+    float gml;
+    const float gm = wave_inclusive_scan2(lg, gml);
+    const float glast = readlane_f(gm, clen - 1), glastl = readlane_f(gml, clen - 1);
     cb.gam[lane] = gm;
+    cb.gaml[lane] = gml;
     cb.bet[lane] = bt;
-    cb.eg[lane] = exp_le0(gm);
-    cb.dd[lane] = exp_le0(glast - gm);
+    cb.eg[lane] = exp2_le0(gm);
+    cb.dd[lane] = exp2_le0(fminf(gamma_diff(glast, glastl, gm, gml), 0.f));
   }
 }
 

@@ -7,6 +7,8 @@ A_log = log U[1, 16]; dt_bias = 0.1 randn; scale = 1/sqrt(128); initial state
 (A_log = log U[0.01, 0.05], g ~ 0.97-0.99) and smaller beta, so that the state
 path (the g*S term, inter-chunk propagation) dominates the outputs -- under the
 default gates one 64-token chunk decays the state by e^-50 or more.
+``gate="edge"`` drives the gate prologue's branches: softplus arguments above 20,
+saturated beta and A_log from no decay at all to a state wiped every token.
 
 All tensors are generated with a seeded ``torch.Generator`` on ``device``.
 """
@@ -42,7 +44,18 @@ def _unit_bf16(shape, gen, device) -> torch.Tensor:
     return x.to(torch.bfloat16)
 
 
+# A_log per v-head under gate="edge", cycled over the heads: no decay at all
+# (exp(A_log) ~ 6e-6, g = 1 to fp32 precision), slow, moderate, the top of the
+# baseline range (log 16) and beyond it (e^4 ~ 55: the state is wiped each token).
+EDGE_A_LOG = (-12.0, -4.0, 0.0, math.log(16.0), 4.0)
+
+
 def _params(hv: int, gate: str, gen, device):
+    if gate == "edge":
+        A_log = torch.tensor([EDGE_A_LOG[h % len(EDGE_A_LOG)] for h in range(hv)],
+                             dtype=torch.float32, device=device)
+        dt_bias = 0.1 * torch.randn(hv, generator=gen, device=device, dtype=torch.float32)
+        return A_log, dt_bias
     if gate == "baseline":
         lo, hi = 1.0, 16.0
     elif gate == "slow":
@@ -53,6 +66,22 @@ def _params(hv: int, gate: str, gen, device):
     A_log = torch.log(lo + (hi - lo) * u)
     dt_bias = 0.1 * torch.randn(hv, generator=gen, device=device, dtype=torch.float32)
     return A_log, dt_bias
+
+
+def _edge_ab(shape, gen, device):
+    """Gate inputs a, b for gate="edge": a mixes N(0,1) with values in [21, 40]
+    (softplus takes its linear branch, x > 20) and with -40 (softplus ~ 4e-18);
+    b mixes N(0,1) with +-12 (beta saturates at 1 - 6e-6 and 6e-6) and +-30."""
+    u = torch.rand(shape, generator=gen, device=device)
+    a = torch.randn(shape, generator=gen, device=device)
+    a = torch.where(u < 0.35, 21.0 + 19.0 * torch.rand(shape, generator=gen, device=device), a)
+    a = torch.where((u >= 0.35) & (u < 0.45), torch.full_like(a, -40.0), a)
+    w = torch.rand(shape, generator=gen, device=device)
+    b = torch.randn(shape, generator=gen, device=device)
+    sgn = torch.where(torch.rand(shape, generator=gen, device=device) < 0.5, -1.0, 1.0)
+    b = torch.where(w < 0.3, 12.0 * sgn, b)
+    b = torch.where((w >= 0.3) & (w < 0.4), 30.0 * sgn, b)
+    return a.to(torch.bfloat16), b.to(torch.bfloat16)
 
 
 def decode_inputs(batch: int, heads: Heads = Heads(), seed: int = 0, device="cpu",
@@ -69,9 +98,12 @@ def decode_inputs(batch: int, heads: Heads = Heads(), seed: int = 0, device="cpu
         "v": torch.randn((B, 1, h.hv, h.dv), generator=gen, device=device).to(torch.bfloat16),
     }
     out["A_log"], out["dt_bias"] = _params(h.hv, gate, gen, device)
-    out["a"] = torch.randn((B, 1, h.hv), generator=gen, device=device).to(torch.bfloat16)
-    bshift = -1.0 if gate == "slow" else 0.0
-    out["b"] = (torch.randn((B, 1, h.hv), generator=gen, device=device) + bshift).to(torch.bfloat16)
+    if gate == "edge":
+        out["a"], out["b"] = _edge_ab((B, 1, h.hv), gen, device)
+    else:
+        out["a"] = torch.randn((B, 1, h.hv), generator=gen, device=device).to(torch.bfloat16)
+        bshift = -1.0 if gate == "slow" else 0.0
+        out["b"] = (torch.randn((B, 1, h.hv), generator=gen, device=device) + bshift).to(torch.bfloat16)
     out["scale"] = 1.0 / math.sqrt(h.dk)
     nstate = pool_slots if pool_slots is not None else B
     if with_state or pool_slots is not None:
@@ -119,9 +151,12 @@ def prefill_inputs(lengths, heads: Heads = Heads(), seed: int = 0, device="cpu",
         "v": torch.randn((T, h.hv, h.dv), generator=gen, device=device).to(torch.bfloat16),
     }
     out["A_log"], out["dt_bias"] = _params(h.hv, gate, gen, device)
-    out["a"] = torch.randn((T, h.hv), generator=gen, device=device).to(torch.bfloat16)
-    bshift = -1.0 if gate == "slow" else 0.0
-    out["b"] = (torch.randn((T, h.hv), generator=gen, device=device) + bshift).to(torch.bfloat16)
+    if gate == "edge":
+        out["a"], out["b"] = _edge_ab((T, h.hv), gen, device)
+    else:
+        out["a"] = torch.randn((T, h.hv), generator=gen, device=device).to(torch.bfloat16)
+        bshift = -1.0 if gate == "slow" else 0.0
+        out["b"] = (torch.randn((T, h.hv), generator=gen, device=device) + bshift).to(torch.bfloat16)
     out["scale"] = 1.0 / math.sqrt(h.dk)
     cu = np.concatenate([[0], np.cumsum(lengths)]).astype(np.int64)
     out["cu_seqlens"] = torch.tensor(cu, dtype=cu_dtype, device=device)

@@ -107,11 +107,16 @@ def test_decode_pooled_matches_oracle(gpu, gate):
 
 
 def test_decode_pooled_config2_full_size(gpu):
-    """BASELINE config 2 (B=512 over a 1024-slot pool): untouched slots are bit-identical;
-    touched slots equal the contiguous decode kernel on the gathered states; a sample of rows
-    matches the oracle."""
+    """BASELINE config 2 (B=512 over a 1024-slot pool): every output row and every touched
+    slot against the oracle (gather -> decode -> scatter); untouched slots bit-identical;
+    touched slots equal the contiguous decode kernel on the gathered states."""
     say("decode pooled config2 full size")
-    w = workloads.decode_inputs(512, seed=2, pool_slots=1024, device=gpu)
+    w = workloads.decode_inputs(512, seed=2, pool_slots=1024)
+    o_ref, pool_ref = O.decode_pooled(*[to_numpy(w[k]) for k in ("q", "k", "v", "state")],
+                                      w["state_indices"].numpy(),
+                                      *[to_numpy(w[k]) for k in ("A_log", "a", "dt_bias", "b")],
+                                      w["scale"])
+    w = {k: (v.to(gpu) if isinstance(v, torch.Tensor) else v) for k, v in w.items()}
     idx = w["state_indices"]
     pool = w["state"].clone()
     out = torch.empty_like(w["v"])
@@ -122,18 +127,28 @@ def test_decode_pooled_config2_full_size(gpu):
     binding.decode_kernel(w["q"], w["k"], w["v"], gathered, w["A_log"], w["a"], w["dt_bias"],
                           w["b"], w["scale"], out2, gathered)
     torch.cuda.synchronize()
+    assert_close(host(out), o_ref, OUT_RTOL, OUT_ATOL, "output")
+    assert_close(host(pool), pool_ref, STATE_RTOL, STATE_ATOL, "pool")
     mask = torch.ones(1024, dtype=torch.bool, device=gpu)
     mask[idx.long()] = False
     assert torch.equal(pool[mask], w["state"][mask])
     assert torch.equal(out, out2)
     assert torch.equal(pool[idx.long()], gathered)
-    sample = [0, 1, 255, 511]
-    sub = {k: (w[k][sample] if k in ("q", "k", "v", "a", "b") else w[k])
-           for k in ("q", "k", "v", "a", "b", "A_log", "dt_bias", "scale")}
-    sub["state"] = w["state"][idx.long()[sample]]
-    o_ref, s_ref = oracle_decode(sub)
-    assert_close(host(out[sample]), o_ref, OUT_RTOL, OUT_ATOL, "output sample")
-    assert_close(host(pool[idx.long()[sample]]), s_ref, STATE_RTOL, STATE_ATOL, "state sample")
+
+
+@pytest.mark.parametrize("B", [1, 8])
+def test_decode_edge_gates(gpu, B):
+    """The gate prologue's edge branches against the oracle: softplus arguments above 20,
+    saturated beta (b = +-12, +-30) and A_log from -12 (no decay) to 4, per v-head."""
+    say(f"decode edge gates B={B}")
+    w = workloads.decode_inputs(B, seed=42, gate="edge", state_scale=0.5)
+    x = to_numpy(w["a"]) + to_numpy(w["dt_bias"])
+    assert (x > 20).any()
+    o_ref, s_ref = oracle_decode(w)
+    out, ns = run_decode(w, gpu, in_place=False)
+    torch.cuda.synchronize()
+    assert_close(host(out), o_ref, OUT_RTOL, OUT_ATOL, "output")
+    assert_close(host(ns), s_ref, STATE_RTOL, STATE_ATOL, "new_state")
 
 
 def test_decode_golden_fixture(gpu):
