@@ -26,6 +26,7 @@ _HEADS = [c_int32, c_int32, c_int32, c_int32, c_int32]
 SIGNATURES = {
     "gdn_version": ([], c_int),
     "gdn_last_error": ([], ctypes.c_char_p),
+    "gdn_build_id": ([], ctypes.c_char_p),
     "gdn_decode": ([_P] * 8 + [c_double, _P, _P, c_int64] + _HEADS + [_P], c_int),
     "gdn_decode_check": ([_P] * 8 + [c_double, _P, _P, c_int64] + _HEADS, c_int),
     "gdn_decode_pooled": ([_P, _P, _P, _P, c_int64, _P, _P, _P, _P, _P, c_double, _P, c_int64]
@@ -39,6 +40,7 @@ SIGNATURES = {
     "gdn_prefill_workspace_size": ([c_int64, c_int64, c_int32], c_int64),
     "gdn_prefill_with_workspace": ([_P] * 8 + [_P, c_int32, c_int64, c_int64, c_double, _P, _P]
                                    + _HEADS + [_P, c_int64, _P], c_int),
+    "gdn_prefill_giveups": ([ctypes.POINTER(ctypes.c_uint64), c_int32], c_int),
     # include/gdn_kernel_amd_testing.h
     "gdn_decode_num_variants": ([], c_int),
     "gdn_decode_with_variant": ([_P] * 8 + [c_double, _P, _P, c_int64] + _HEADS + [c_int32, _P], c_int),

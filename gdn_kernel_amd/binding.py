@@ -30,7 +30,7 @@ import torch
 
 from . import _lib
 
-__all__ = ["decode_kernel", "decode_pooled_kernel", "prefill_kernel", "GDNError"]
+__all__ = ["decode_kernel", "decode_pooled_kernel", "prefill_kernel", "prefill_giveups", "GDNError"]
 
 GDNError = _lib.GDNError
 _BF16 = torch.bfloat16
@@ -220,3 +220,19 @@ def prefill_kernel(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, outp
                                             _ptr(new_state), Hq, Hk, Hv, dk, dv, _ptr(ws), ws_bytes,
                                             _stream(dev))
     _lib.check(rc)
+
+
+def prefill_giveups(reset: bool = False, device=None) -> int:
+    """Number of prefill wavefronts on ``device`` (default: the current one) whose
+    hand-off wait gave up since the library was loaded or the last reset
+    (gdn_prefill_giveups).  Synchronises the device.  A give-up, which only a defect
+    could cause, leaves NaN in the affected outputs and final states; 0 means every
+    launch so far completed its hand-offs."""
+    import ctypes
+    lib = _lib.load()
+    dev = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
+    count = ctypes.c_uint64(0)
+    with _on_device(dev):
+        rc = lib.gdn_prefill_giveups(ctypes.byref(count), 1 if reset else 0)
+    _lib.check(rc)
+    return int(count.value)

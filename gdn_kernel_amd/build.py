@@ -6,6 +6,7 @@ source tree; there is no JIT cache and no installation step.
 """
 from __future__ import annotations
 
+import hashlib
 import os
 import shutil
 import subprocess
@@ -33,6 +34,25 @@ HIPCC_FLAGS = [
 ]
 
 
+# Everything the library's code depends on, relative to the repository root: the
+# C headers and the HIP/C++ sources and headers.
+BUILD_INPUTS = ["include/gdn_kernel_amd.h", "include/gdn_kernel_amd_testing.h",
+                *(f"gdn_kernel_amd/csrc/{f}" for f in SOURCES + HEADERS)]
+
+
+def source_digest(root: Path | None = None) -> str:
+    """Build id of the library: 16 hex digits of SHA-256 over the build inputs under
+    ``root`` (default: this tree), each as path, NUL, content, NUL, then the
+    compiler flags.  Compiled into the library (gdn_build_id), so a library can be
+    matched with the exact sources it was built from."""
+    root = Path(root) if root is not None else PKG_DIR.parent
+    h = hashlib.sha256()
+    for rel in BUILD_INPUTS:
+        h.update(rel.encode() + b"\0" + (root / rel).read_bytes() + b"\0")
+    h.update(" ".join(HIPCC_FLAGS).encode())
+    return h.hexdigest()[:16]
+
+
 def hipcc() -> str:
     for cand in (os.environ.get("HIPCC"), "/opt/rocm/bin/hipcc", shutil.which("hipcc")):
         if cand and Path(cand).exists():
@@ -45,7 +65,8 @@ def build(verbose: bool = False, out: Path | None = None) -> Path:
     out = Path(out) if out else LIB_PATH
     tmp = out.with_suffix(".so.tmp")
     srcs = [str(CSRC / s) for s in SOURCES]
-    cmd = [hipcc(), *HIPCC_FLAGS, "-I", str(PKG_DIR.parent / "include"), *srcs, "-o", str(tmp)]
+    cmd = [hipcc(), *HIPCC_FLAGS, f'-DGDN_BUILD_ID="{source_digest()}"', "-I",
+           str(PKG_DIR.parent / "include"), *srcs, "-o", str(tmp)]
     if verbose:
         print(" ".join(cmd), flush=True)
     res = subprocess.run(cmd, capture_output=True, text=True)

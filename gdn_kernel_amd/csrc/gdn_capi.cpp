@@ -30,6 +30,9 @@ int ok() {
 
 constexpr int kD = 128;
 constexpr int64_t kMaxGrid = 0x7fffffff;
+// A launch's grid times its workgroup size (work-items per dimension) must fit in
+// 32 bits.
+constexpr int64_t kMaxWorkItems = 0xffffffffLL;
 
 int check_heads(int32_t hq, int32_t hk, int32_t hv, int32_t dk, int32_t dv) {
   if (hq <= 0 || hk <= 0 || hv <= 0)
@@ -74,6 +77,52 @@ int device_status(hipError_t e, const char* what) {
   return ok();
 }
 
+// The decode grid of `variant` (or of the launcher's own pick, variant < 0) for
+// batch * num_v_heads heads must fit: work-items in 32 bits (and the batch in an int).
+int check_decode_launch(int64_t batch, int32_t num_v_heads, int variant) {
+  const int64_t heads = batch * num_v_heads;
+  const int vi = variant >= 0 ? variant : gdn::decode_pick_variant(heads);
+  const int64_t per_head = gdn::decode_items_per_head(vi);
+  if (batch > kMaxGrid || heads > kMaxWorkItems / per_head)
+    return fail(GDN_ERR_INVALID_ARGUMENT,
+                "batch * num_v_heads = %lld is too large: the launch would need %lld work-items per "
+                "head, at most %lld in total",
+                (long long)heads, (long long)per_head, (long long)kMaxWorkItems);
+  return GDN_OK;
+}
+
+int decode_check_impl(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v, const float* state,
+                      const float* A_log, const gdn_bf16* a, const float* dt_bias, const gdn_bf16* b,
+                      double scale, gdn_bf16* output, float* new_state, int64_t batch, int32_t num_q_heads,
+                      int32_t num_k_heads, int32_t num_v_heads, int32_t head_dim_k, int32_t head_dim_v,
+                      int variant) {
+  if (batch < 0) return fail(GDN_ERR_INVALID_ARGUMENT, "batch must be >= 0 (got %lld)", (long long)batch);
+  GDN_TRY(check_heads(num_q_heads, num_k_heads, num_v_heads, head_dim_k, head_dim_v));
+  GDN_TRY(check_scale(scale));
+  if (batch == 0) return ok();
+  if (!q || !k || !v || !A_log || !a || !dt_bias || !b || !output || !new_state)
+    return fail(GDN_ERR_INVALID_ARGUMENT, "null tensor pointer (only state may be null)");
+  GDN_TRY(check_decode_launch(batch, num_v_heads, variant));
+  GDN_TRY(check_alias(state, new_state, batch * num_v_heads * int64_t(kD) * kD * 4, "new_state"));
+  return ok();
+}
+
+int decode_pooled_check_impl(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v, float* state_pool,
+                             int64_t pool_slots, const int32_t* state_indices, const float* A_log,
+                             const gdn_bf16* a, const float* dt_bias, const gdn_bf16* b, double scale,
+                             gdn_bf16* output, int64_t batch, int32_t num_q_heads, int32_t num_k_heads,
+                             int32_t num_v_heads, int32_t head_dim_k, int32_t head_dim_v, int variant) {
+  if (batch < 0) return fail(GDN_ERR_INVALID_ARGUMENT, "batch must be >= 0 (got %lld)", (long long)batch);
+  if (pool_slots <= 0) return fail(GDN_ERR_INVALID_ARGUMENT, "pool_slots must be > 0 (got %lld)", (long long)pool_slots);
+  GDN_TRY(check_heads(num_q_heads, num_k_heads, num_v_heads, head_dim_k, head_dim_v));
+  GDN_TRY(check_scale(scale));
+  if (batch == 0) return ok();
+  if (!q || !k || !v || !state_pool || !state_indices || !A_log || !a || !dt_bias || !b || !output)
+    return fail(GDN_ERR_INVALID_ARGUMENT, "null tensor pointer");
+  GDN_TRY(check_decode_launch(batch, num_v_heads, variant));
+  return ok();
+}
+
 }  // namespace
 
 extern "C" {
@@ -82,20 +131,17 @@ int gdn_version(void) { return 100; }
 
 const char* gdn_last_error(void) { return g_err; }
 
+#ifndef GDN_BUILD_ID
+#define GDN_BUILD_ID "unknown"
+#endif
+const char* gdn_build_id(void) { return GDN_BUILD_ID; }
+
 int gdn_decode_check(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v, const float* state,
                      const float* A_log, const gdn_bf16* a, const float* dt_bias, const gdn_bf16* b,
                      double scale, gdn_bf16* output, float* new_state, int64_t batch, int32_t num_q_heads,
                      int32_t num_k_heads, int32_t num_v_heads, int32_t head_dim_k, int32_t head_dim_v) {
-  if (batch < 0) return fail(GDN_ERR_INVALID_ARGUMENT, "batch must be >= 0 (got %lld)", (long long)batch);
-  GDN_TRY(check_heads(num_q_heads, num_k_heads, num_v_heads, head_dim_k, head_dim_v));
-  GDN_TRY(check_scale(scale));
-  if (batch == 0) return ok();
-  if (!q || !k || !v || !A_log || !a || !dt_bias || !b || !output || !new_state)
-    return fail(GDN_ERR_INVALID_ARGUMENT, "null tensor pointer (only state may be null)");
-  if (batch * num_v_heads * (kD / 8) > kMaxGrid)
-    return fail(GDN_ERR_INVALID_ARGUMENT, "batch * num_v_heads too large (%lld)", (long long)(batch * num_v_heads));
-  GDN_TRY(check_alias(state, new_state, batch * num_v_heads * int64_t(kD) * kD * 4, "new_state"));
-  return ok();
+  return decode_check_impl(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state, batch, num_q_heads,
+                           num_k_heads, num_v_heads, head_dim_k, head_dim_v, -1);
 }
 
 int gdn_decode_pooled_check(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v, float* state_pool,
@@ -103,16 +149,9 @@ int gdn_decode_pooled_check(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16
                             const gdn_bf16* a, const float* dt_bias, const gdn_bf16* b, double scale,
                             gdn_bf16* output, int64_t batch, int32_t num_q_heads, int32_t num_k_heads,
                             int32_t num_v_heads, int32_t head_dim_k, int32_t head_dim_v) {
-  if (batch < 0) return fail(GDN_ERR_INVALID_ARGUMENT, "batch must be >= 0 (got %lld)", (long long)batch);
-  if (pool_slots <= 0) return fail(GDN_ERR_INVALID_ARGUMENT, "pool_slots must be > 0 (got %lld)", (long long)pool_slots);
-  GDN_TRY(check_heads(num_q_heads, num_k_heads, num_v_heads, head_dim_k, head_dim_v));
-  GDN_TRY(check_scale(scale));
-  if (batch == 0) return ok();
-  if (!q || !k || !v || !state_pool || !state_indices || !A_log || !a || !dt_bias || !b || !output)
-    return fail(GDN_ERR_INVALID_ARGUMENT, "null tensor pointer");
-  if (batch * num_v_heads * (kD / 8) > kMaxGrid)
-    return fail(GDN_ERR_INVALID_ARGUMENT, "batch * num_v_heads too large (%lld)", (long long)(batch * num_v_heads));
-  return ok();
+  return decode_pooled_check_impl(q, k, v, state_pool, pool_slots, state_indices, A_log, a, dt_bias, b, scale,
+                                  output, batch, num_q_heads, num_k_heads, num_v_heads, head_dim_k, head_dim_v,
+                                  -1);
 }
 
 int gdn_prefill_check(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v, const float* state,
@@ -131,8 +170,11 @@ int gdn_prefill_check(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v, c
   GDN_TRY(check_heads(num_q_heads, num_k_heads, num_v_heads, head_dim_k, head_dim_v));
   GDN_TRY(check_scale(scale));
   if (num_seqs == 0) return ok();
-  if (num_seqs * num_v_heads > kMaxGrid)
-    return fail(GDN_ERR_INVALID_ARGUMENT, "num_seqs * num_v_heads too large");
+  if (num_seqs > kMaxGrid || num_seqs * num_v_heads > kMaxGrid ||
+      gdn::prefill_work_items(num_seqs * num_v_heads) > kMaxWorkItems)
+    return fail(GDN_ERR_INVALID_ARGUMENT,
+                "num_seqs * num_v_heads = %lld is too large: the launch would exceed %lld work-items",
+                (long long)(num_seqs * num_v_heads), (long long)kMaxWorkItems);
   if (!cu_seqlens || !A_log || !dt_bias || !new_state)
     return fail(GDN_ERR_INVALID_ARGUMENT, "null tensor pointer (only state may be null)");
   if (total_tokens > 0 && (!q || !k || !v || !a || !b || !output))
@@ -149,8 +191,8 @@ int decode_impl(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v, const f
                 const float* A_log, const gdn_bf16* a, const float* dt_bias, const gdn_bf16* b, double scale,
                 gdn_bf16* output, float* new_state, int64_t batch, int32_t num_q_heads, int32_t num_k_heads,
                 int32_t num_v_heads, int32_t head_dim_k, int32_t head_dim_v, int variant, void* stream) {
-  GDN_TRY(gdn_decode_check(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state, batch, num_q_heads,
-                           num_k_heads, num_v_heads, head_dim_k, head_dim_v));
+  GDN_TRY(decode_check_impl(q, k, v, state, A_log, a, dt_bias, b, scale, output, new_state, batch, num_q_heads,
+                            num_k_heads, num_v_heads, head_dim_k, head_dim_v, variant));
   if (batch == 0) return ok();
   gdn::DecodeArgs args{};
   args.q = q; args.k = k; args.v = v;
@@ -168,8 +210,9 @@ int decode_pooled_impl(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v, 
                        const float* dt_bias, const gdn_bf16* b, double scale, gdn_bf16* output, int64_t batch,
                        int32_t num_q_heads, int32_t num_k_heads, int32_t num_v_heads, int32_t head_dim_k,
                        int32_t head_dim_v, int variant, void* stream) {
-  GDN_TRY(gdn_decode_pooled_check(q, k, v, state_pool, pool_slots, state_indices, A_log, a, dt_bias, b, scale,
-                                  output, batch, num_q_heads, num_k_heads, num_v_heads, head_dim_k, head_dim_v));
+  GDN_TRY(decode_pooled_check_impl(q, k, v, state_pool, pool_slots, state_indices, A_log, a, dt_bias, b, scale,
+                                   output, batch, num_q_heads, num_k_heads, num_v_heads, head_dim_k, head_dim_v,
+                                   variant));
   if (batch == 0) return ok();
   gdn::DecodeArgs args{};
   args.q = q; args.k = k; args.v = v;
@@ -272,6 +315,11 @@ int gdn_prefill_with_workspace(const gdn_bf16* q, const gdn_bf16* k, const gdn_b
   return prefill_impl(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu_seqlens_dtype, num_seqs, total_tokens,
                       scale, output, new_state, num_q_heads, num_k_heads, num_v_heads, head_dim_k, head_dim_v, 0, 0,
                       nullptr, workspace, workspace_bytes, stream);
+}
+
+int gdn_prefill_giveups(uint64_t* count, int32_t reset) {
+  if (!count) return fail(GDN_ERR_INVALID_ARGUMENT, "count must not be null");
+  return device_status(gdn::prefill_giveups(count, reset != 0), "gdn_prefill_giveups");
 }
 
 int gdn_decode_num_variants(void) { return gdn::kDecodeVariants; }

@@ -157,15 +157,28 @@ hipError_t launch_variant(const DecodeArgs& a, hipStream_t stream) {
 
 }  // namespace
 
+int decode_pick_variant(int64_t heads) {
+  // Measured on MI355X (B=64 and pooled B=512, cold cache): 8 rows per wave,
+  // 4 waves, nontemporal state traffic is fastest; small batches use one-wave
+  // workgroups so that more CUs get work.
+  return heads >= 128 ? 1 : 8;
+}
+
+int64_t decode_items_per_head(int variant) {
+  switch (variant) {
+#define GDN_ITEMS(I, R, W, NT) \
+  case I:                      \
+    return kHeadDim / (R) * 64;
+    GDN_DECODE_VARIANTS(GDN_ITEMS)
+#undef GDN_ITEMS
+    default:
+      return kHeadDim / 16 * 64;
+  }
+}
+
 hipError_t launch_decode(const DecodeArgs& a, hipStream_t stream, int variant) {
   int vi = variant;
-  if (vi < 0 || vi >= kDecodeVariants) {
-    const int64_t heads = int64_t(a.B) * a.Hv;
-    // Measured on MI355X (B=64 and pooled B=512, cold cache): 8 rows per wave,
-    // 4 waves, nontemporal state traffic is fastest; small batches use one-wave
-    // workgroups so that more CUs get work.
-    vi = heads >= 128 ? 1 : 8;
-  }
+  if (vi < 0 || vi >= kDecodeVariants) vi = decode_pick_variant(int64_t(a.B) * a.Hv);
   switch (vi) {
 #define GDN_CASE(I, R, W, NT) \
   case I:                     \

@@ -59,6 +59,21 @@ int64_t prefill_workspace_bytes(int N, int64_t T, int Hv);
 // access), numbered 0 .. kDecodeVariants-1; variant < 0 picks by batch size.
 constexpr int kDecodeVariants = 16;
 hipError_t launch_decode(const DecodeArgs& args, hipStream_t stream, int variant = -1);
+
+// The decode launch shape used for `heads` = B * Hv (b, v-head) pairs when no
+// variant is requested, and the work-items one head takes in a variant (the grid
+// is heads * decode_items_per_head(v) / block work-items).
+int decode_pick_variant(int64_t heads);
+int64_t decode_items_per_head(int variant);
+
+// Work-items of a prefill main-kernel launch for this many (sequence, v-head)
+// chains on the current device (the grid times the workgroup size of the variant
+// the launcher picks).
+int64_t prefill_work_items(int64_t chains);
 hipError_t launch_prefill(const PrefillArgs& args, hipStream_t stream);
+
+// Waves of prefill launches on the current device whose hand-off wait gave up,
+// since the library was loaded or the last reset; synchronises the device first.
+hipError_t prefill_giveups(uint64_t* count, bool reset);
 
 }  // namespace gdn

@@ -367,6 +367,14 @@ __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
+}  // namespace
+
+// Waves on this device whose hand-off wait gave up (see wait_count), since the
+// library was loaded or the count was last reset; read by prefill_giveups.
+__device__ unsigned int gdn_prefill_giveup_count;
+
+namespace {
+
 // Hand-off between the two roles: monotonically increasing LDS counters.  A wave
 // signals by adding 1 after all its earlier LDS accesses completed (release); a
 // waiter polls until the count reaches its target (acquire).
@@ -382,9 +390,12 @@ __device__ __forceinline__ void signal_count(Smem& sm, int which, int lane) {
 // Waits until counter `which` reaches `target`.  Every wait is bounded: if one
 // ever gives up (which only a logic error, or the testing hooks of PrefillArgs,
 // can cause), it raises kAbort, and all later waits return at once, so the
-// workgroup still finishes (with wrong results) instead of hanging.  Production
-// kernels give up after kSpinLimit polls; kernels built with the hooks after
-// sm.spin_limit polls, counting each give-up in sm.aborts if set.
+// workgroup still finishes instead of hanging.  The wave that gives up adds 1 to
+// gdn_prefill_giveup_count (a global atomic from one lane), and the workgroup
+// writes NaN to every output element and state element it owns (and the prep
+// kernel NaN images), so wrong results never look valid.  Production kernels give
+// up after kSpinLimit polls; kernels built with the hooks after sm.spin_limit
+// polls, also counting each give-up in sm.aborts if set.
 template <bool kHooks, class Smem>
 __device__ __forceinline__ void wait_count(Smem& sm, int which, int target) {
   if (__hip_atomic_load(&sm.sync[which], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) < target) {
@@ -394,10 +405,12 @@ __device__ __forceinline__ void wait_count(Smem& sm, int which, int target) {
       if (__hip_atomic_load(&sm.sync[kAbort], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != 0) break;
       if (it >= (kHooks ? sm.spin_limit : kSpinLimit)) {
         __hip_atomic_store(&sm.sync[kAbort], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-        if constexpr (kHooks) {
-          unsigned* aborts = sm.aborts;
-          if (aborts && __builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)) == 0)
-            __hip_atomic_fetch_add(aborts, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+        if (__builtin_amdgcn_mbcnt_hi(~0u, __builtin_amdgcn_mbcnt_lo(~0u, 0u)) == 0) {
+          __hip_atomic_fetch_add(&gdn_prefill_giveup_count, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          if constexpr (kHooks) {
+            unsigned* aborts = sm.aborts;
+            if (aborts) __hip_atomic_fetch_add(aborts, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+          }
         }
         break;
       }
@@ -405,6 +418,13 @@ __device__ __forceinline__ void wait_count(Smem& sm, int which, int target) {
   }
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 }
+
+template <class Smem>
+__device__ __forceinline__ bool aborted(Smem& sm) {
+  return __hip_atomic_load(&sm.sync[kAbort], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != 0;
+}
+
+constexpr uint32_t kNaNx2 = 0x7fc07fc0u;  // two bf16 quiet NaNs
 
 #ifdef GDN_PREFILL_PHASE_CLOCKS
 // Development builds only (-DGDN_PREFILL_PHASE_CLOCKS): core-clock cycles that
@@ -803,12 +823,13 @@ __device__ __forceinline__ void stage_kq_gates(const ChunkBufs& cb, const Produc
 }
 
 // Producer thread pt's share of a chunk's T~ hi, T~ lo and P tiles (their LDS
-// images) to the chunk's image in the workspace.
-__device__ __forceinline__ void copy_tiles_out(const ChunkBufs& cb, u32x4* image, int pt) {
+// images) to the chunk's image in the workspace; NaN images once a hand-off wait
+// of the workgroup gave up.
+__device__ __forceinline__ void copy_tiles_out(const ChunkBufs& cb, u32x4* image, int pt, bool poison) {
   constexpr int NT1 = C * TSTR / 8;
   for (int e = pt; e < kTileImage; e += NPROD) {
     const uint16_t* src = e < NT1 ? cb.Th + 8 * e : e < 2 * NT1 ? cb.Tl + 8 * (e - NT1) : cb.P + 8 * (e - 2 * NT1);
-    image[e] = *reinterpret_cast<const u32x4*>(src);
+    image[e] = poison ? u32x4{kNaNx2, kNaNx2, kNaNx2, kNaNx2} : *reinterpret_cast<const u32x4*>(src);
   }
 }
 
@@ -861,7 +882,7 @@ __device__ __forceinline__ void producer_loop(Smem& sm, const PrefillArgs& p, in
     if constexpr (V::kCopy) {
       if (t >= 1) {
         wait_count<V::kHooks>(sm, kReady, 4 * t);  // chunk t - 1 handed over by all four waves
-        copy_tiles_out(chunk_bufs(sm, (t - 1) & 1), images + int64_t(t - 1) * p.Hv * kTileImage, pt);
+        copy_tiles_out(chunk_bufs(sm, (t - 1) & 1), images + int64_t(t - 1) * p.Hv * kTileImage, pt, aborted(sm));
       }
     }
     clk.lap(0);
@@ -979,7 +1000,8 @@ __device__ __forceinline__ void producer_loop(Smem& sm, const PrefillArgs& p, in
   }
   if constexpr (V::kCopy) {
     wait_count<V::kHooks>(sm, kReady, 4 * nchunks);
-    copy_tiles_out(chunk_bufs(sm, (nchunks - 1) & 1), images + int64_t(nchunks - 1) * p.Hv * kTileImage, pt);
+    copy_tiles_out(chunk_bufs(sm, (nchunks - 1) & 1), images + int64_t(nchunks - 1) * p.Hv * kTileImage, pt,
+                   aborted(sm));
   }
   clk.store(V::NCW + pw, lane0);
 }
@@ -1379,7 +1401,27 @@ __global__ __launch_bounds__(V::NTHREADS) void gdn_prefill_kernel(PrefillArgs p)
       }
     }
   }
-  if (nchunks > 0) consumer_loop<V>(sm, p, s0, s1, nchunks, h, row0, wave, lane0, S);
+  if (nchunks > 0) {
+    consumer_loop<V>(sm, p, s0, s1, nchunks, h, row0, wave, lane0, S);
+    if (aborted(sm)) {
+      // A hand-off wait gave up: NaN over every output element of this wave (all
+      // chunks of the sequence, its state rows of head h) and its state slice.
+      const int64_t vstride = int64_t(p.Hv) * D;
+      uint16_t* obase = p.out + int64_t(h) * D + row0 + VW * wave + (VT == 2 ? 8 : 4) * (lane0 >> 4);
+      for (int64_t tok = s0 + n16; tok < s1; tok += 16) {
+        if constexpr (VT == 2) {
+          *reinterpret_cast<uint4*>(obase + tok * vstride) = uint4{kNaNx2, kNaNx2, kNaNx2, kNaNx2};
+        } else {
+          *reinterpret_cast<uint2*>(obase + tok * vstride) = uint2{kNaNx2, kNaNx2};
+        }
+      }
+      const float nan = __builtin_nanf("");
+#pragma unroll
+      for (int vt = 0; vt < VT; ++vt)
+#pragma unroll
+        for (int kt = 0; kt < 8; ++kt) S[vt][kt] = f32x4{nan, nan, nan, nan};
+    }
+  }
 
   // Final state (for an empty sequence: the initial state, or zeros).
   if (nchunks > 0 || p.state != p.new_state) {
@@ -1468,6 +1510,22 @@ int device_cus() {
 
 }  // namespace
 
+// Reads (and with `reset` clears) this device's give-up count, after
+// synchronising the device so that every launch so far has finished.
+hipError_t prefill_giveups(uint64_t* count, bool reset) {
+  hipError_t e = hipDeviceSynchronize();
+  if (e != hipSuccess) return e;
+  unsigned int v = 0;
+  e = hipMemcpyFromSymbol(&v, HIP_SYMBOL(gdn_prefill_giveup_count), sizeof(v));
+  if (e != hipSuccess) return e;
+  *count = v;
+  if (reset) {
+    const unsigned int z = 0;
+    e = hipMemcpyToSymbol(HIP_SYMBOL(gdn_prefill_giveup_count), &z, sizeof(z));
+  }
+  return e;
+}
+
 #ifndef GDN_PREFILL_MAX_SPLIT
 #define GDN_PREFILL_MAX_SPLIT 8
 #endif
@@ -1482,6 +1540,21 @@ int split_factor(int64_t chains) {
   return F;
 }
 
+}  // namespace
+
+int64_t prefill_work_items(int64_t chains) {
+  if (chains <= 0) return 0;
+  const int F = split_factor(chains);
+  const int64_t grid = F == 1 ? chains : (chains + 7) / 8 * 8 * F;
+  switch (F) {
+    case 1: return grid * Variant<4, 2>::NTHREADS;
+    case 2: return grid * Variant<4, 1>::NTHREADS;
+    case 4: return grid * Variant<2, 1>::NTHREADS;
+    default: return grid * Variant<1, 1>::NTHREADS;
+  }
+}
+
+namespace {
 // Largest workspace the two-kernel path uses; bigger batches take one kernel.
 constexpr int64_t kMaxWorkspaceBytes = int64_t(2) << 30;
 }  // namespace

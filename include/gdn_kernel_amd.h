@@ -43,6 +43,11 @@ int gdn_version(void);
 /* Message describing the last failure on the calling thread ("" if none). */
 const char* gdn_last_error(void);
 
+/* Build id: 16 hex digits of SHA-256 over the headers, sources and compiler flags
+ * the library was built from (gdn_kernel_amd.build.source_digest), so a built
+ * library can be matched with its sources.  No reference counterpart. */
+const char* gdn_build_id(void);
+
 /*
  * Decode step, destination-passing.  Replaces the reference's TVM-FFI export
  * `kernel` = GDNDecodeKernel (solution/cuda/kernel.cu:101-113, exported at
@@ -159,6 +164,23 @@ int gdn_prefill_with_workspace(const gdn_bf16* q, const gdn_bf16* k, const gdn_b
                                int32_t num_q_heads, int32_t num_k_heads, int32_t num_v_heads,
                                int32_t head_dim_k, int32_t head_dim_v, void* workspace,
                                int64_t workspace_bytes, void* stream);
+
+
+/*
+ * Failure report of the prefill kernels' hand-off waits.  No reference
+ * counterpart: the reference prefill kernel synchronises with workgroup barriers
+ * only (kernel_prefill.cu:149-161) and has no bounded wait that could fail.
+ * Here the wavefronts of a prefill workgroup hand chunks to each other through
+ * bounded waits (about 70 ms of polling).  A wait that gives up -- which only a
+ * defect could cause -- lets the workgroup finish instead of hanging the GPU; the
+ * workgroup then writes NaN to every output and final-state element it owns, and
+ * each wavefront that gave up adds 1 to a counter on the device.
+ * gdn_prefill_giveups synchronises the current device, stores that counter (the
+ * give-ups since the library was loaded, or since the last reset) in *count, and
+ * with reset != 0 clears it.  A launch that returned GDN_OK and left the counter
+ * at 0 completed every hand-off.
+ */
+int gdn_prefill_giveups(uint64_t* count, int32_t reset);
 
 #ifdef __cplusplus
 }

@@ -11,6 +11,23 @@ if ROOT not in sys.path:
 
 def pytest_configure(config):
     config.addinivalue_line("markers", "gpu: needs a ROCm GPU (MI355X); run with -m gpu")
+    config.addinivalue_line("markers", "giveups_expected: a GPU test that makes prefill hand-off "
+                                       "waits give up on purpose (through the testing hooks)")
+
+
+@pytest.fixture(autouse=True)
+def _no_prefill_giveups(request):
+    """Around every GPU test: no prefill hand-off wait may give up (the device counter
+    that gdn_prefill_giveups reads stays at 0), except in tests that force give-ups
+    through the testing hooks and check the count themselves."""
+    if request.node.get_closest_marker("gpu") is None or \
+            request.node.get_closest_marker("giveups_expected") is not None:
+        yield
+        return
+    from gdn_kernel_amd import binding
+    binding.prefill_giveups(reset=True)
+    yield
+    assert binding.prefill_giveups() == 0, "a prefill hand-off wait gave up during this test"
 
 
 @pytest.fixture(scope="session")

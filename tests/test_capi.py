@@ -204,3 +204,43 @@ def test_check_maps_codes_to_exceptions():
         _lib.check(UNSUPPORTED)
     with pytest.raises(_lib.GDNError):
         _lib.check(_lib.GDN_ERR_DEVICE)
+
+
+def test_launch_size_is_bounded_in_work_items(lib):
+    """A launch's grid times its workgroup size must fit in 32 bits.  Decode takes 1024
+    work-items per (batch row, v-head) in its default launch shape (8 rows per
+    wavefront), so B * Hv may reach 4,194,303; shapes with 2 rows per wavefront take
+    4096 (B * Hv up to 1,048,575).  Prefill's one-kernel launch takes 512 per (sequence,
+    v-head) chain, so N * Hv may reach 8,388,607.  Larger requests are rejected before
+    any device call instead of failing at launch."""
+    assert lib.gdn_decode_check(*dec_args(B=131071, state=None)) == OK          # 4,194,272 heads
+    assert lib.gdn_decode_check(*dec_args(B=131072, state=None)) == INVALID     # 4,194,304
+    assert "work-items" in _lib.last_error()
+    assert lib.gdn_decode(*dec_args(B=131072, state=None), None) == INVALID
+    assert lib.gdn_decode_pooled_check(*pool_args(B=131071)) == OK
+    assert lib.gdn_decode_pooled_check(*pool_args(B=131072)) == INVALID
+    assert lib.gdn_decode_pooled(*pool_args(B=131072), None) == INVALID
+    # variant 15: 2 rows per wavefront, one wavefront per workgroup
+    assert lib.gdn_decode_with_variant(*dec_args(B=32768, state=None), 15, None) == INVALID
+    assert "work-items" in _lib.last_error()
+    assert lib.gdn_decode_pooled_with_variant(*pool_args(B=32768), 15, None) == INVALID
+    assert lib.gdn_prefill_check(*pre_args(N=262143, state=None)) == OK           # 8,388,576 chains
+    assert lib.gdn_prefill_check(*pre_args(N=262144, state=None)) == INVALID      # 8,388,608
+    assert "work-items" in _lib.last_error()
+    assert lib.gdn_prefill(*pre_args(N=262144, state=None), None) == INVALID
+
+
+def test_prefill_giveups_reporting(lib):
+    """gdn_prefill_giveups (the device count of prefill hand-off waits that gave up)
+    rejects a null destination before any device call; without a usable GPU it reports
+    a device error with a message instead of a count, and the Python helper raises."""
+    assert lib.gdn_prefill_giveups(None, 0) == INVALID
+    assert "count" in _lib.last_error()
+    count = ctypes.c_uint64(12345)
+    rc = lib.gdn_prefill_giveups(ctypes.byref(count), 0)
+    assert rc in (OK, _lib.GDN_ERR_DEVICE)
+    if rc == OK:
+        assert count.value < 12345
+    else:
+        assert "gdn_prefill_giveups" in _lib.last_error()
+        assert count.value == 12345

@@ -65,3 +65,7 @@ def test_extracted_tree_builds_and_exports_the_c_abi(tmp_path):
     header = (ROOT / "include" / "gdn_kernel_amd.h").read_text()
     for name in re.findall(r"^\w[\w\s\*]*?\b(gdn_\w+)\(", header, re.M):
         assert hasattr(lib, name), name
+    # the extracted tree's build carries the id of its inputs, which are this tree's
+    from gdn_kernel_amd import build
+    lib.gdn_build_id.restype = ctypes.c_char_p
+    assert lib.gdn_build_id().decode() == build.source_digest(tmp_path / "x") == build.source_digest()

@@ -392,20 +392,25 @@ def test_prefill_workspace_reuse(gpu):
         assert torch.equal(o, ref_o) and torch.equal(s, ref_s), f"{name}: workspace path differs"
 
 
+@pytest.mark.giveups_expected
 def test_prefill_bounded_waits(gpu):
     """The hand-off failure path, forced from the host.  With the testing hooks off
-    the entry point is gdn_prefill bit for bit.  With the producers signalling only
-    their first chunk and a 2,000-poll wait limit, every workgroup of a sequence with
-    two or more chunks has a consumer wait that can only give up: the launch still
-    completes (every wait is bounded), the give-ups are counted, the one-chunk
-    sequence's results are untouched, and the next normal launch is exact again."""
+    the entry point is gdn_prefill bit for bit and nothing gives up.  With the
+    producers signalling only their first chunk and a 2,000-poll wait limit, every
+    workgroup of a sequence with two or more chunks has a consumer wait that can only
+    give up: the launch still completes (every wait is bounded), the give-ups are
+    counted both by the hook counter and by the device counter that
+    gdn_prefill_giveups reports, every output and final-state element of the affected
+    sequences is NaN, the one-chunk sequence's results are untouched, and the next
+    normal launch is exact again."""
     lens = [300, 130, 40]             # 5, 3 and 1 chunks; 96 chains: split 2 ways
     p = workloads.prefill_inputs(lens, seed=21, gate="slow", state_scale=0.5)
+    binding.prefill_giveups(reset=True)
     say("prefill bounded waits: hooks off")
     o0, s0, a0 = _prefill_fault_injection(p, gpu, 0, 0)
     o1, s1 = run_prefill(p, gpu)
     torch.cuda.synchronize()
-    assert int(a0.item()) == 0
+    assert int(a0.item()) == 0 and binding.prefill_giveups() == 0
     assert torch.equal(o0, o1) and torch.equal(s0, s1)
     say("prefill bounded waits: chunk-ready signals stop after chunk 0, 2000-poll limit")
     o2, s2, a2 = _prefill_fault_injection(p, gpu, 2000, 1)
@@ -413,12 +418,16 @@ def test_prefill_bounded_waits(gpu):
     waiting_wgs = 2 * 32 * 2          # sequences with >= 2 chunks x v-heads x workgroups per chain
     n = int(a2.item())
     assert waiting_wgs <= n <= waiting_wgs * 8, n
+    assert binding.prefill_giveups(reset=True) == n, "the device counter must see every give-up"
     s, e = sum(lens[:2]), sum(lens)
+    assert torch.isnan(o2[:s].float()).all() and torch.isnan(s2[:2]).all(), \
+        "outputs and states of the sequences whose waits gave up must be NaN"
     assert torch.equal(o2[s:e], o1[s:e]) and torch.equal(s2[2], s1[2])
     say("prefill bounded waits: a normal launch afterwards")
     o3, s3 = run_prefill(p, gpu)
     torch.cuda.synchronize()
     assert torch.equal(o3, o1) and torch.equal(s3, s1)
+    assert binding.prefill_giveups() == 0
 
 
 @pytest.mark.parametrize("seed", range(6))

@@ -69,3 +69,33 @@ def test_shim_signature_and_calls(op):
     called = set(re.findall(r"\b(gdn_[a-z_0-9]+)\s*\(", src))
     assert called == {f"gdn_{op}", "gdn_last_error"}
     assert _call_arity(src, f"gdn_{op}") == _declared_arity(f"gdn_{op}")
+
+
+EXPECTED_DTYPES = {
+    "decode": {"q": "kBF16", "k": "kBF16", "v": "kBF16", "state": "kF32", "A_log": "kF32",
+               "a": "kBF16", "dt_bias": "kF32", "b": "kBF16", "output": "kBF16", "new_state": "kF32"},
+    "prefill": {"q": "kBF16", "k": "kBF16", "v": "kBF16", "state": "kF32", "A_log": "kF32",
+                "a": "kBF16", "dt_bias": "kF32", "b": "kBF16", "cu_seqlens": "kIndex",
+                "output": "kBF16", "new_state": "kF32"},
+}
+
+
+@pytest.mark.parametrize("op", ["decode", "prefill"])
+def test_shim_checks_every_tensor(op):
+    """Before the C-ABI call each shim checks every tensor argument (check_tensor: dtype,
+    rank, extents, device, contiguity) with the dtype the binding requires, the
+    optional state only when it is not a null tensor, as binding.py does."""
+    src = _strip_comments((b.CSRC / b.TVM_FFI_SHIMS[op]).read_text())
+    calls = dict(re.findall(r'check_tensor\(\s*(\w+)\s*,\s*"\1"\s*,\s*DType::(\w+)', src))
+    assert calls == EXPECTED_DTYPES[op]
+    assert re.search(r"if\s*\(\s*state\.data_ptr\(\)\s*!=\s*nullptr\s*\)\s*check_tensor\(\s*state", src)
+    assert src.index("check_tensor(new_state") < src.index(f"gdn_{op}(")
+
+
+def test_check_helper_covers_dtype_rank_device_contiguity():
+    src = _strip_comments((b.CSRC / "tvm_ffi" / "check.hpp").read_text())
+    body = src[src.index("inline void check_tensor"):]
+    for needle in ("dtype_ok(t.dtype()", "t.ndim()", "t.size(i)", "t.device()", "t.stride(j)",
+                   "TVM_FFI_THROW(ValueError)"):
+        assert needle in body, needle
+    assert "kDLBfloat" in src and "kDLFloat" in src and "kDLInt" in src
