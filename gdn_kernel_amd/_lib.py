@@ -41,6 +41,8 @@ SIGNATURES = {
     "gdn_prefill_with_workspace": ([_P] * 8 + [_P, c_int32, c_int64, c_int64, c_double, _P, _P]
                                    + _HEADS + [_P, c_int64, _P], c_int),
     "gdn_prefill_giveups": ([ctypes.POINTER(ctypes.c_uint64), c_int32], c_int),
+    "gdn_prefill_no_alloc": ([_P] * 8 + [_P, c_int32, c_int64, c_int64, c_double, _P, _P] + _HEADS
+                             + [_P], c_int),
     # include/gdn_kernel_amd_testing.h
     "gdn_decode_num_variants": ([], c_int),
     "gdn_decode_with_variant": ([_P] * 8 + [c_double, _P, _P, c_int64] + _HEADS + [c_int32, _P], c_int),

@@ -33,6 +33,8 @@ constexpr int64_t kMaxGrid = 0x7fffffff;
 // A launch's grid times its workgroup size (work-items per dimension) must fit in
 // 32 bits.
 constexpr int64_t kMaxWorkItems = 0xffffffffLL;
+static_assert(GDN_PREFILL_NO_ALLOC_SCRATCH_BYTES == gdn::kPrefillScratchBytes,
+              "the header's scratch size must match the library's");
 
 int check_heads(int32_t hq, int32_t hk, int32_t hv, int32_t dk, int32_t dv) {
   if (hq <= 0 || hk <= 0 || hv <= 0)
@@ -315,6 +317,28 @@ int gdn_prefill_with_workspace(const gdn_bf16* q, const gdn_bf16* k, const gdn_b
   return prefill_impl(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu_seqlens_dtype, num_seqs, total_tokens,
                       scale, output, new_state, num_q_heads, num_k_heads, num_v_heads, head_dim_k, head_dim_v, 0, 0,
                       nullptr, workspace, workspace_bytes, stream);
+}
+
+int gdn_prefill_no_alloc(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v, const float* state,
+                         const float* A_log, const gdn_bf16* a, const float* dt_bias, const gdn_bf16* b,
+                         const void* cu_seqlens, int32_t cu_seqlens_dtype, int64_t num_seqs, int64_t total_tokens,
+                         double scale, gdn_bf16* output, float* new_state, int32_t num_q_heads,
+                         int32_t num_k_heads, int32_t num_v_heads, int32_t head_dim_k, int32_t head_dim_v,
+                         void* stream) {
+  GDN_TRY(gdn_prefill_check(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu_seqlens_dtype, num_seqs,
+                            total_tokens, scale, output, new_state, num_q_heads, num_k_heads, num_v_heads,
+                            head_dim_k, head_dim_v));
+  const int64_t need = num_seqs > 0 ? gdn::prefill_workspace_bytes(int(num_seqs), total_tokens, num_v_heads) : 0;
+  if (need > gdn::kPrefillScratchBytes)
+    return fail(GDN_ERR_INVALID_ARGUMENT,
+                "this batch needs %lld bytes of chunk images, more than the %lld-byte scratch of "
+                "gdn_prefill_no_alloc; use gdn_prefill_with_workspace (or gdn_prefill)",
+                static_cast<long long>(need), static_cast<long long>(gdn::kPrefillScratchBytes));
+  void* ws = nullptr;
+  if (need > 0) GDN_TRY(device_status(gdn::prefill_scratch(&ws), "gdn_prefill_no_alloc: scratch address"));
+  return prefill_impl(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu_seqlens_dtype, num_seqs, total_tokens,
+                      scale, output, new_state, num_q_heads, num_k_heads, num_v_heads, head_dim_k, head_dim_v, 0, 0,
+                      nullptr, ws, need, stream);
 }
 
 int gdn_prefill_giveups(uint64_t* count, int32_t reset) {

@@ -72,6 +72,11 @@ int64_t decode_items_per_head(int variant);
 int64_t prefill_work_items(int64_t chains);
 hipError_t launch_prefill(const PrefillArgs& args, hipStream_t stream);
 
+// Bytes of the per-device scratch array of gdn_prefill_no_alloc, and its address
+// on the current device (looked up on the first call per device).
+constexpr int64_t kPrefillScratchBytes = int64_t(64) << 20;
+hipError_t prefill_scratch(void** ptr);
+
 // Waves of prefill launches on the current device whose hand-off wait gave up,
 // since the library was loaded or the last reset; synchronises the device first.
 hipError_t prefill_giveups(uint64_t* count, bool reset);

@@ -1510,6 +1510,34 @@ int device_cus() {
 
 }  // namespace
 
+// Scratch of gdn_prefill_no_alloc: the chunk images of the two-kernel path, for
+// callers that cannot allocate.  Each device that loads the library holds its own
+// copy until the process ends; every call on a device shares it.
+static __device__ __align__(256) uint8_t scratch[kPrefillScratchBytes];
+
+namespace {
+constexpr int kMaxDevices = 64;
+}  // namespace
+
+// The device address of `scratch` on the current device, looked up once per
+// device (with that device current) and kept.  In host code `scratch` names a
+// host-side stand-in, so kernels and copies must use this address instead.
+hipError_t prefill_scratch(void** ptr) {
+  static std::atomic<void*> addr[kMaxDevices];  // null until looked up; racing lookups store the same value
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  void* p = addr[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return e;
+    addr[dev].store(p, std::memory_order_release);
+  }
+  *ptr = p;
+  return hipSuccess;
+}
+
 // Reads (and with `reset` clears) this device's give-up count, after
 // synchronising the device so that every launch so far has finished.
 hipError_t prefill_giveups(uint64_t* count, bool reset) {

@@ -165,6 +165,29 @@ int gdn_prefill_with_workspace(const gdn_bf16* q, const gdn_bf16* k, const gdn_b
                                int32_t head_dim_k, int32_t head_dim_v, void* workspace,
                                int64_t workspace_bytes, void* stream);
 
+/*
+ * gdn_prefill_with_workspace for callers that cannot allocate device memory
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid
+ * hipMalloc).  No counterpart in the reference, which has no workspace.  Same
+ * arguments and results as gdn_prefill (bit for bit); the chunk images of the
+ * two-kernel path live in a scratch array that the library holds on each device
+ * (GDN_PREFILL_NO_ALLOC_SCRATCH_BYTES, allocated when the library's code is
+ * loaded onto the device and kept until the process ends).  Nothing is allocated
+ * per call.  A batch whose images need more than that (gdn_prefill_workspace_size
+ * above it) returns GDN_ERR_INVALID_ARGUMENT; batches that gdn_prefill serves with
+ * one kernel need no scratch.  Every call on a device shares that device's
+ * scratch: calls that overlap on one GPU (launched on different streams without
+ * ordering between them) race and give wrong results.
+ */
+#define GDN_PREFILL_NO_ALLOC_SCRATCH_BYTES (64LL << 20)
+
+int gdn_prefill_no_alloc(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v,
+                         const float* state, const float* A_log, const gdn_bf16* a,
+                         const float* dt_bias, const gdn_bf16* b, const void* cu_seqlens,
+                         int32_t cu_seqlens_dtype, int64_t num_seqs, int64_t total_tokens,
+                         double scale, gdn_bf16* output, float* new_state,
+                         int32_t num_q_heads, int32_t num_k_heads, int32_t num_v_heads,
+                         int32_t head_dim_k, int32_t head_dim_v, void* stream);
 
 /*
  * Failure report of the prefill kernels' hand-off waits.  No reference
