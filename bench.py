@@ -14,8 +14,9 @@ chunked prefill tokens/s on the 32-sequence / 32768-token varlen batch and on
 the single 4096-token sequence (with MFMA-roofline fractions computed from the
 algorithmic 180,224 FLOP per token and v-head), the rates this box measures on
 library work (a device copy and a bf16 GEMM, ``measured_peaks``) with the roofline
-fractions against them, and the CPU baseline (the numpy oracle, the reference decode
-definition restated, timed on the host).
+fractions against them, and the CPU baseline (the reference's PyTorch decode definition
+restated, fp32 on every host core this process may use; the numpy oracle on one thread
+is reported beside it).
 
 Usage: python bench.py [--gpus 1] [--steps K] [--warmup W] [--only decode|prefill]
        [--no-cpu] [--cpu-seconds S]
@@ -219,17 +220,38 @@ def bench_pooled(args, torch, binding, workloads):
                 frac=nbytes / (ev_mean * 1e-3) / 1e9 / HBM_PEAK_GBS, bytes=nbytes)
 
 
-def bench_prefill(args, torch, binding, workloads, cfg):
+def bench_prefill(args, torch, binding, workloads, cfg, path="drop-in"):
+    """Prefill on config ``cfg`` through ``path``: "drop-in" (the reference-signature
+    ``kernel``, gdn_prefill), "workspace" (gdn_prefill_with_workspace with a
+    preallocated workspace) or "no-alloc" (gdn_prefill_no_alloc, the library's
+    scratch)."""
     dev = torch.device("cuda:0")
     p = workloads.config(cfg, device=dev)
     T = p["q"].shape[0]
     N = p["cu_seqlens"].numel() - 1
     out = torch.empty((T, HV, D), dtype=torch.bfloat16, device=dev)
     ns = torch.empty((N, HV, D, D), dtype=torch.float32, device=dev)
+    args_ = (p["q"], p["k"], p["v"], p["state"], p["A_log"], p["a"], p["dt_bias"], p["b"],
+             p["cu_seqlens"], p["scale"], out, ns)
+    if path == "drop-in":
+        def step(i):
+            binding.prefill_kernel(*args_)
+    elif path == "workspace":
+        ws = torch.empty(binding.prefill_workspace_bytes(N, T, HV), dtype=torch.uint8, device=dev)
 
-    def step(i):
-        binding.prefill_kernel(p["q"], p["k"], p["v"], p["state"], p["A_log"], p["a"],
-                               p["dt_bias"], p["b"], p["cu_seqlens"], p["scale"], out, ns)
+        def step(i):
+            binding.prefill_kernel_with_workspace(*args_, ws)
+    else:
+        from gdn_kernel_amd import _lib
+        lib = _lib.load()
+        ptr = lambda t: None if t is None else t.data_ptr()
+        cargs = [ptr(p[k]) for k in ("q", "k", "v", "state", "A_log", "a", "dt_bias", "b")]
+        cargs += [p["cu_seqlens"].data_ptr(), _lib.GDN_INDEX_INT32, N, T, p["scale"], ptr(out),
+                  ptr(ns), HQ, HK, HV, D, D]
+        stream = torch.cuda.current_stream(dev).cuda_stream
+
+        def step(i):
+            _lib.check(lib.gdn_prefill_no_alloc(*cargs, stream))
 
     # Untimed warm-up for at least PREFILL_WARM_S (the GPU leaves its idle clocks
     # within the first few hundred milliseconds), then `steps` timed launches.
@@ -249,7 +271,59 @@ def bench_prefill(args, torch, binding, workloads, cfg):
                 lengths=p["lengths"] if cfg == 4 else None)
 
 
-def cpu_baseline(seconds, workloads):
+def cpu_model():
+    """The host CPU's model name as /proc/cpuinfo reports it for the first processor
+    (with its family and model numbers), else platform's description."""
+    info = {}
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if not line.strip():
+                    break
+                key, _, val = line.partition(":")
+                info.setdefault(key.strip(), val.strip())
+    except OSError:
+        pass
+    name = info.get("model name") or platform.processor() or platform.machine()
+    if "cpu family" in info:
+        return f"{name} (family {info['cpu family']}, model {info.get('model', '?')})"
+    return name
+
+
+def cpu_baseline(seconds, workloads, torch):
+    """BASELINE config 0 (B=1, heads 16/16/32) through the reference's PyTorch decode
+    definition (design.md:166-226, restated in oracle/torch_definition.py), fp32 on the
+    host CPU with torch's thread pool on every core this process may run on
+    (len(os.sched_getaffinity(0))): one warm-up run, then the median of at least 5 runs
+    over about ``seconds``."""
+    from oracle.torch_definition import decode_definition
+    cores = len(os.sched_getaffinity(0))
+    prev = torch.get_num_threads()
+    torch.set_num_threads(cores)
+    try:
+        w = workloads.config(0)
+        args = [w[k] for k in ("q", "k", "v", "state", "A_log", "a", "dt_bias", "b", "scale")]
+        decode_definition(*args)
+        times = []
+        t_end = time.perf_counter() + seconds
+        while time.perf_counter() < t_end or len(times) < 5:
+            t0 = time.perf_counter()
+            decode_definition(*args)
+            times.append(time.perf_counter() - t0)
+    finally:
+        torch.set_num_threads(prev)
+    med = float(np.median(times))
+    nbytes = decode_bytes(1)
+    return {"value": nbytes / med / 1e9, "unit": "GB/s", "cores": cores, "kind": "port",
+            "us_per_step": med * 1e6,
+            "sample": (f"reference PyTorch decode definition (design.md:166-226), fp32, "
+                       f"torch.set_num_threads({cores}), on config 0: B=1, 32 v-heads, "
+                       f"{nbytes} algorithmic bytes/step; median of {len(times)} steps after "
+                       f"1 warm-up, over ~{seconds:.0f} s"),
+            "cpu_model": cpu_model()}
+
+
+def cpu_baseline_numpy(seconds, workloads):
     """The oracle's decode (design.md:166-226 restated in numpy, fp32 arithmetic like the
     reference's .float() path) on BASELINE config 0 (B=1), single-threaded."""
     from threadpoolctl import threadpool_limits
@@ -267,21 +341,11 @@ def cpu_baseline(seconds, workloads):
             times.append(time.perf_counter() - t0)
     med = float(np.median(times))
     nbytes = decode_bytes(1)
-    cpu = platform.processor() or platform.machine()
-    try:
-        with open("/proc/cpuinfo") as f:
-            for line in f:
-                if line.startswith("model name"):
-                    cpu = line.split(":", 1)[1].strip()
-                    break
-    except OSError:
-        pass
     return {"value": nbytes / med / 1e9, "unit": "GB/s", "cores": 1, "kind": "port",
             "us_per_step": med * 1e6,
             "sample": (f"oracle decode (numpy fp32, 1 thread) on config 0: B=1, 32 v-heads, "
                        f"{nbytes} algorithmic bytes/step; median of {len(times)} steps over "
-                       f"~{seconds:.0f} s"),
-            "cpu_model": cpu}
+                       f"~{seconds:.0f} s")}
 
 
 def cpu_baseline_prefill(seconds, workloads):
@@ -366,8 +430,13 @@ def main():
         res["decode_pooled_b512"] = {k: (round(v, 4) if isinstance(v, float) else v)
                                      for k, v in pooled.items()}
     if args.only in ("prefill", "all"):
-        for cfg, key in ((4, "prefill_varlen_32k"), (3, "prefill_t4096")):
-            pr = bench_prefill(args, torch, binding, workloads, cfg)
+        for cfg, key, path in ((4, "prefill_varlen_32k", "drop-in"), (3, "prefill_t4096", "drop-in"),
+                               (3, "prefill_t4096_workspace", "workspace"),
+                               (3, "prefill_t4096_no_alloc", "no-alloc")):
+            pr = bench_prefill(args, torch, binding, workloads, cfg, path)
+            pr["path"] = {"drop-in": "kernel (gdn_prefill, as the TVM-FFI shim)",
+                          "workspace": "kernel_with_workspace (gdn_prefill_with_workspace)",
+                          "no-alloc": "gdn_prefill_no_alloc (library scratch)"}[path]
             res[key] = {k: (round(v, 4) if isinstance(v, float) else v) for k, v in pr.items()}
         if res["value"] is None:
             res["value"] = round(res["prefill_varlen_32k"]["tokens_per_s"], 1)
@@ -379,11 +448,13 @@ def main():
     res["measured_peaks"] = peaks
     if "roofline" in res:
         res["roofline"]["frac_of_measured_copy"] = round(res["roofline"]["achieved"] / peaks["copy_gbs"], 4)
-    for key in ("prefill_varlen_32k", "prefill_t4096"):
+    for key in ("prefill_varlen_32k", "prefill_t4096", "prefill_t4096_workspace",
+                "prefill_t4096_no_alloc"):
         if key in res:
             res[key]["frac_of_measured_gemm"] = round(res[key]["tflops"] / peaks["bf16_gemm_tflops"], 4)
     if not args.no_cpu:
-        res["cpu_baseline"] = cpu_baseline(args.cpu_seconds, workloads)
+        res["cpu_baseline"] = cpu_baseline(args.cpu_seconds, workloads, torch)
+        res["cpu_baseline_numpy_1t"] = cpu_baseline_numpy(args.cpu_seconds / 2, workloads)
         if args.only in ("prefill", "all"):
             res["cpu_baseline_prefill"] = cpu_baseline_prefill(args.cpu_seconds / 2, workloads)
     print(json.dumps(res), flush=True)

@@ -11,6 +11,9 @@ Mirrors the reference's entry points argument for argument:
 * ``decode_pooled_kernel(q, k, v, state_pool, A_log, a, dt_bias, b, scale,
   output, state_indices)`` -- no reference counterpart; decode over an indexed
   state pool, updated in place.
+* ``prefill_kernel_with_workspace(..., new_state, workspace)`` -- no reference
+  counterpart; ``prefill_kernel`` with a caller-owned workspace, which batches of
+  few chains use to prepare each chunk once.
 
 Semantics kept from the reference: outputs are preallocated and written in
 place; ``scale`` None or 0 selects 1/sqrt(dk); ``state`` None means a zero
@@ -30,7 +33,8 @@ import torch
 
 from . import _lib
 
-__all__ = ["decode_kernel", "decode_pooled_kernel", "prefill_kernel", "prefill_giveups", "GDNError"]
+__all__ = ["decode_kernel", "decode_pooled_kernel", "prefill_kernel", "prefill_kernel_with_workspace",
+           "prefill_workspace_bytes", "prefill_giveups", "GDNError"]
 
 GDNError = _lib.GDNError
 _BF16 = torch.bfloat16
@@ -164,23 +168,18 @@ def decode_pooled_kernel(q, k, v, state_pool, A_log, a, dt_bias, b, scale, outpu
     _lib.check(rc)
 
 
-def prefill_kernel(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output,
-                   new_state) -> None:
-    """Varlen chunked prefill over packed sequences (kernel_prefill.cu:300-306).
-    q,k [T,H{q,k},128] bf16 (a leading batch dim of 1 is accepted); v [T,Hv,128]
-    bf16; state [N,Hv,128,128] fp32 or None; a,b [T,Hv] bf16; cu_seqlens [N+1]
-    int32 or int64 on the device; output [T,Hv,128] bf16; new_state
-    [N,Hv,128,128] fp32 (may be ``state``).  Batches of few (sequence, head)
-    chains take a workspace from torch's caching allocator (gdn_prefill_with_workspace)."""
+def _prefill_args(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, output, new_state):
+    """Validate the prefill arguments; returns (device, C-ABI argument list without the
+    stream)."""
     dev = _device_of(q)
 
-    def squeeze1(t, name, nd):
+    def squeeze1(t, nd):
         if t is not None and t.dim() == nd + 1 and t.shape[0] == 1:
             return t[0]
         return t
 
-    q, k, v = squeeze1(q, "q", 3), squeeze1(k, "k", 3), squeeze1(v, "v", 3)
-    a, b, output = squeeze1(a, "a", 2), squeeze1(b, "b", 2), squeeze1(output, "output", 3)
+    q, k, v = squeeze1(q, 3), squeeze1(k, 3), squeeze1(v, 3)
+    a, b, output = squeeze1(a, 2), squeeze1(b, 2), squeeze1(output, 3)
     if q.dim() != 3 or k.dim() != 3 or v.dim() != 3:
         raise ValueError("q, k, v must be [T, H, d] (optionally with a leading 1)")
     T, Hq, dk = q.shape
@@ -208,16 +207,54 @@ def prefill_kernel(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, outp
     _need(b, "b", _BF16, (T, Hv), dev)
     _need(output, "output", _BF16, (T, Hv, dv), dev)
     _need(new_state, "new_state", _F32, (N, Hv, dv, dk), dev)
+    return dev, [_ptr(q), _ptr(k), _ptr(v), _ptr(state), _ptr(A_log), _ptr(a), _ptr(dt_bias),
+                 _ptr(b), cu_seqlens.data_ptr(), cu_code, N, T, None, _ptr(output),
+                 _ptr(new_state), Hq, Hk, Hv, dk, dv]
+
+
+def prefill_kernel(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output,
+                   new_state) -> None:
+    """Varlen chunked prefill over packed sequences (kernel_prefill.cu:300-306), the
+    drop-in ``kernel``.  q,k [T,H{q,k},128] bf16 (a leading batch dim of 1 is
+    accepted); v [T,Hv,128] bf16; state [N,Hv,128,128] fp32 or None; a,b [T,Hv] bf16;
+    cu_seqlens [N+1] int32 or int64 on the device; output [T,Hv,128] bf16; new_state
+    [N,Hv,128,128] fp32 (may be ``state``).  Calls gdn_prefill, as the TVM-FFI shim
+    does: nothing is allocated, and calls on any streams are independent."""
+    dev, args = _prefill_args(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, output, new_state)
+    args[12] = _scale(scale)
     lib = _lib.load()
     with _on_device(dev):
-        # Batches of few (sequence, head) chains prepare their chunks in a first
-        # kernel; its workspace comes from torch's caching allocator on this stream.
-        ws_bytes = lib.gdn_prefill_workspace_size(N, T, Hv)
-        ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev) if ws_bytes > 0 else None
-        rc = lib.gdn_prefill_with_workspace(_ptr(q), _ptr(k), _ptr(v), _ptr(state), _ptr(A_log),
-                                            _ptr(a), _ptr(dt_bias), _ptr(b), cu_seqlens.data_ptr(),
-                                            cu_code, N, T, _scale(scale), _ptr(output),
-                                            _ptr(new_state), Hq, Hk, Hv, dk, dv, _ptr(ws), ws_bytes,
+        rc = lib.gdn_prefill(*args, _stream(dev))
+    _lib.check(rc)
+
+
+def prefill_workspace_bytes(num_seqs: int, total_tokens: int, num_v_heads: int, device=None) -> int:
+    """Bytes of workspace ``prefill_kernel_with_workspace`` uses for a batch of this size on
+    ``device`` (gdn_prefill_workspace_size); 0 when the batch runs one kernel anyway."""
+    lib = _lib.load()
+    dev = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
+    with _on_device(dev):
+        return int(lib.gdn_prefill_workspace_size(num_seqs, total_tokens, num_v_heads))
+
+
+def prefill_kernel_with_workspace(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, output,
+                                  new_state, workspace) -> None:
+    """``prefill_kernel`` with a caller-owned device workspace (gdn_prefill_with_workspace;
+    no reference counterpart): batches of few (sequence, v-head) chains then prepare
+    each chunk once in a first kernel, for the same results bit for bit.  ``workspace``
+    is a contiguous uint8 tensor of at least ``prefill_workspace_bytes(N, T, Hv)`` bytes
+    on the same device (or None: ``prefill_kernel``); launches that may overlap must
+    not share one."""
+    dev, args = _prefill_args(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, output, new_state)
+    args[12] = _scale(scale)
+    if workspace is not None:
+        if not isinstance(workspace, torch.Tensor) or workspace.dtype != torch.uint8 or \
+                workspace.dim() != 1 or workspace.device != dev or not workspace.is_contiguous():
+            raise ValueError("workspace must be a contiguous 1-D uint8 tensor on the device of q")
+    lib = _lib.load()
+    with _on_device(dev):
+        rc = lib.gdn_prefill_with_workspace(*args, _ptr(workspace),
+                                            0 if workspace is None else workspace.numel(),
                                             _stream(dev))
     _lib.check(rc)
 

@@ -22,6 +22,15 @@ def test_binding_rejects_cpu_tensors():
                                torch.empty_like(p["v"]), torch.empty_like(p["state"]))
 
 
+def test_prefill_with_workspace_checks_arguments():
+    p = workloads.prefill_inputs([3, 5], seed=0)
+    with pytest.raises(ValueError, match="GPU"):
+        binding.prefill_kernel_with_workspace(
+            p["q"], p["k"], p["v"], p["state"], p["A_log"], p["a"], p["dt_bias"], p["b"],
+            p["cu_seqlens"], p["scale"], torch.empty_like(p["v"]), torch.empty_like(p["state"]),
+            torch.empty(16, dtype=torch.uint8))
+
+
 def test_entry_points_have_reference_arity():
     import inspect
     from gdn_kernel_amd import decode, prefill

@@ -3,7 +3,7 @@ work and synchronisations in between) must reproduce the eager result bit for bi
 import pytest
 import torch
 
-from gdn_kernel_amd import binding, workloads
+from gdn_kernel_amd import _lib, binding, workloads
 from tests.gpu_util import say
 
 pytestmark = pytest.mark.gpu
@@ -48,21 +48,39 @@ def test_decode_graph_replays_match_eager(gpu):
         assert torch.isfinite(x)
 
 
+@pytest.mark.parametrize("path", ["drop-in", "workspace", "no-alloc"])
 @pytest.mark.parametrize("lens", [[130, 3, 0, 64], [300]])
-def test_prefill_graph_replays_match_eager(gpu, lens):
-    """128 chains (one kernel) and 32 chains (two kernels: the Python kernel takes the
-    workspace from torch's allocator, which during capture is the graph's own pool)."""
-    say(f"prefill graph replay lens={lens}")
+def test_prefill_graph_replays_match_eager(gpu, lens, path):
+    """128 chains (one kernel) and 32 chains (split 8 ways), through the drop-in kernel
+    (gdn_prefill), with a preallocated workspace (two kernels for 32 chains), and through
+    gdn_prefill_no_alloc (two kernels in the library's scratch, nothing allocated during
+    capture)."""
+    say(f"prefill graph replay lens={lens} path={path}")
     p = workloads.prefill_inputs(lens, seed=32, device=gpu, gate="slow", state_scale=0.5)
     T, N = p["q"].shape[0], len(p["lengths"])
     out = torch.empty((T, 32, 128), dtype=torch.bfloat16, device=gpu)
     ns = torch.empty((N, 32, 128, 128), dtype=torch.float32, device=gpu)
+    args = (p["q"], p["k"], p["v"], p["state"], p["A_log"], p["a"], p["dt_bias"], p["b"],
+            p["cu_seqlens"], p["scale"], out, ns)
+    if path == "drop-in":
+        def step():
+            binding.prefill_kernel(*args)
+    elif path == "workspace":
+        ws = torch.empty(binding.prefill_workspace_bytes(N, T, 32), dtype=torch.uint8, device=gpu)
 
-    def step():
-        binding.prefill_kernel(p["q"], p["k"], p["v"], p["state"], p["A_log"], p["a"],
-                               p["dt_bias"], p["b"], p["cu_seqlens"], p["scale"], out, ns)
+        def step():
+            binding.prefill_kernel_with_workspace(*args, ws)
+    else:
+        lib = _lib.load()
+        ptr = lambda t: None if t is None else t.data_ptr()
+        cargs = [ptr(p[k]) for k in ("q", "k", "v", "state", "A_log", "a", "dt_bias", "b")]
+        cargs += [p["cu_seqlens"].data_ptr(), _lib.GDN_INDEX_INT32, N, T, p["scale"], ptr(out),
+                  ptr(ns), 16, 16, 32, 128, 128]
 
-    step()
+        def step():
+            _lib.check(lib.gdn_prefill_no_alloc(*cargs, torch.cuda.current_stream().cuda_stream))
+
+    binding.prefill_kernel(*args)                            # the drop-in's result is the reference
     torch.cuda.synchronize()
     ref_o, ref_s = out.clone(), ns.clone()
     g = _capture(step)

@@ -426,3 +426,26 @@ def test_chunk_checks_catch_dropped_inter_decay():
     bad["A_log"] = np.full_like(c["A_log"], -np.inf)
     o2, _ = O.prefill_chunked(**bad)
     assert not close_report(o2, o1, 1e-6, 1e-8)[0]
+
+
+@pytest.mark.parametrize("gate", ["baseline", "slow", "edge"])
+def test_torch_definition_matches_oracle_decode(gate):
+    """oracle/torch_definition.py (the PyTorch definition of design.md:166-226 that the
+    CPU baseline times) computes what the numpy oracle's decode computes: the same fp32
+    arithmetic up to summation order, on config-0 heads (16/16/32) and two batch rows."""
+    from gdn_kernel_amd import workloads
+    from gdn_kernel_amd.workloads import to_numpy
+    from oracle.torch_definition import decode_definition
+    w = workloads.decode_inputs(2, seed=90, gate=gate, state_scale=0.5)
+    o_t, s_t = decode_definition(w["q"], w["k"], w["v"], w["state"], w["A_log"], w["a"],
+                                 w["dt_bias"], w["b"], w["scale"])
+    o_ref, s_ref = O.decode(*[to_numpy(w[k]) for k in ("q", "k", "v", "state", "A_log", "a",
+                                                        "dt_bias", "b")], w["scale"])
+    assert o_t.dtype == torch.bfloat16 and s_t.dtype == torch.float32
+    assert np.allclose(o_t.double().numpy(), o_ref, rtol=1e-2, atol=1e-2)
+    assert np.allclose(s_t.double().numpy(), s_ref, rtol=1e-5, atol=1e-6)
+    o0, s0 = decode_definition(w["q"], w["k"], w["v"], None, w["A_log"], w["a"], w["dt_bias"],
+                               w["b"], 0.0)
+    z = O.decode(*[to_numpy(w[k]) for k in ("q", "k", "v")], None,
+                 *[to_numpy(w[k]) for k in ("A_log", "a", "dt_bias", "b")], None)
+    assert np.allclose(s0.double().numpy(), z[1], rtol=1e-5, atol=1e-6)
