@@ -1315,7 +1315,8 @@ __device__ int pick_sequence(PrefillSmem& sm, const PrefillArgs& p, int rank, in
 // Workgroup b handles slice f of chain `chain` (chain = rank-major, v-head
 // minor).  With F > 1 the F slices of a chain are b = 8 F (chain / 8) + 8 f +
 // chain % 8: workgroups are dealt to the XCDs round-robin, so the slices of one
-// chain share an XCD (and its L2) for their common K/Q/V reads.
+// chain share an XCD (and its L2) for their common K/Q/V reads.  With F == 1 the
+// two chains of a GQA pair share an XCD the same way.
 template <class V>
 __global__ __launch_bounds__(V::NTHREADS) void gdn_prefill_kernel(PrefillArgs p) {
   constexpr int NCW = V::NCW, VT = V::VT, VW = V::VW, NTHREADS = V::NTHREADS;
@@ -1332,7 +1333,11 @@ __global__ __launch_bounds__(V::NTHREADS) void gdn_prefill_kernel(PrefillArgs p)
   const int wave = !(V::kLoad && NCW == 1) ? hw : hw == 3 ? 0 : hw < 3 ? hw + 1 : hw;
 
   const int bid = blockIdx.x;
-  const int chain = V::F == 1 ? bid : (bid / (8 * V::F)) * 8 + bid % 8;
+  // F == 1: blocks b and b + 8 of each group of 16 take chains 2m and 2m + 1 (v-heads
+  // 2j, 2j + 1, which read the same K and Q): workgroups are dealt to the 8 XCDs
+  // round-robin, so the two start together on one XCD and share its L2.
+  const int chain = V::F == 1 ? (bid & ~15) | ((bid & 7) << 1) | ((bid >> 3) & 1)
+                              : (bid / (8 * V::F)) * 8 + bid % 8;
   const int row0 = V::F == 1 ? 0 : ((bid / 8) % V::F) * V::ROWS;
   if (chain >= p.N * p.Hv) return;  // padding of the last group of eight chains (workgroup-uniform)
   const int h = chain % p.Hv;
@@ -1490,7 +1495,7 @@ __global__ __launch_bounds__(PrepVariant::NTHREADS) void gdn_prefill_prep_kernel
 template <class V>
 hipError_t launch_variant(const PrefillArgs& a, hipStream_t stream) {
   const int64_t chains = int64_t(a.N) * a.Hv;
-  const int64_t grid = V::F == 1 ? chains : (chains + 7) / 8 * 8 * V::F;
+  const int64_t grid = V::F == 1 ? (chains + 15) / 16 * 16 : (chains + 7) / 8 * 8 * V::F;
   hipLaunchKernelGGL(gdn_prefill_kernel<V>, dim3(unsigned(grid)), dim3(V::NTHREADS), 0, stream, a);
   return hipGetLastError();
 }
@@ -1573,7 +1578,7 @@ int split_factor(int64_t chains) {
 int64_t prefill_work_items(int64_t chains) {
   if (chains <= 0) return 0;
   const int F = split_factor(chains);
-  const int64_t grid = F == 1 ? chains : (chains + 7) / 8 * 8 * F;
+  const int64_t grid = F == 1 ? (chains + 15) / 16 * 16 : (chains + 7) / 8 * 8 * F;
   switch (F) {
     case 1: return grid * Variant<4, 2>::NTHREADS;
     case 2: return grid * Variant<4, 1>::NTHREADS;
