@@ -56,8 +56,9 @@ def parse():
     ap.add_argument("--cpu-seconds", type=float, default=10.0)
     ap.add_argument("--pmc-run", action="store_true",
                     help="short fixed launch sequence for rocprofv3 --pmc runs: a torch copy of "
-                         "COPY_BYTES (counter calibration), then 5 decode B=64 launches and 2 "
-                         "prefill launches of the 32k varlen batch; prints nothing")
+                         "COPY_BYTES (counter calibration), then 5 decode B=64 launches, 2 "
+                         "prefill launches of the 32k varlen batch and 2 of the T=4096 "
+                         "sequence (drop-in kernel); prints nothing")
     return ap.parse_args()
 
 
@@ -87,6 +88,14 @@ def pmc_run(torch, binding, workloads):
     p = workloads.config(4, device=dev)
     po = torch.empty((p["q"].shape[0], HV, D), dtype=torch.bfloat16, device=dev)
     ns = torch.empty_like(p["state"])
+    for _ in range(2):
+        flush.fill_(1.0)
+        binding.prefill_kernel(p["q"], p["k"], p["v"], p["state"], p["A_log"], p["a"],
+                               p["dt_bias"], p["b"], p["cu_seqlens"], p["scale"], po, ns)
+    torch.cuda.synchronize()
+    p = workloads.config(3, device=dev)
+    po = torch.empty((p["q"].shape[0], HV, D), dtype=torch.bfloat16, device=dev)
+    ns = torch.empty((1, HV, D, D), dtype=torch.float32, device=dev)
     for _ in range(2):
         flush.fill_(1.0)
         binding.prefill_kernel(p["q"], p["k"], p["v"], p["state"], p["A_log"], p["a"],
