@@ -794,10 +794,36 @@ __device__ __forceinline__ void producer_prefetch(const PrefillArgs& p, int64_t 
   }
 }
 
+// The gates of token `lane` of a chunk (first producer wave, from the raw a/b
+// values of its prefetch): the log2-gate prefix sum as an fp32 pair, beta,
+// e^gamma and the update decay e^{gamma_last - gamma}.
+struct ChunkGates {
+  float gam, gaml, bet, eg, dd;
+};
+
+__device__ __forceinline__ ChunkGates chunk_gates(const ProducerPrefetch& f, int lane, int clen, float neg_decay,
+                                                  float dt_bias) {
+  const float lg = lane < clen ? fast_log2_gate(neg_decay, bf16_to_f32(f.a) + dt_bias) : 0.f;
+  ChunkGates g;
+  g.bet = lane < clen ? fast_sigmoid(bf16_to_f32(f.b)) : 0.f;
+  g.gam = wave_inclusive_scan2(lg, g.gaml);
+  const float glast = readlane_f(g.gam, clen - 1), glastl = readlane_f(g.gaml, clen - 1);
+  g.eg = exp2_le0(g.gam);
+  g.dd = exp2_le0(fminf(gamma_diff(glast, glastl, g.gam, g.gaml), 0.f));
+  return g;
+}
+
+__device__ __forceinline__ void store_gates(const ChunkBufs& cb, const ChunkGates& g, int lane) {
+  cb.gam[lane] = g.gam;
+  cb.gaml[lane] = g.gaml;
+  cb.bet[lane] = g.bet;
+  cb.eg[lane] = g.eg;
+  cb.dd[lane] = g.dd;
+}
+
 // Step 1 of a chunk: the prefetched K and Q rows into the chunk's tiles
-// (permuted columns) and, on the first wave, the chunk's gates.
-__device__ __forceinline__ void stage_kq_gates(const ChunkBufs& cb, const ProducerPrefetch& f, int pt, int pw, int lane,
-                                               int clen, float neg_decay, float dt_bias) {
+// (permuted columns).
+__device__ __forceinline__ void stage_kq(const ChunkBufs& cb, const ProducerPrefetch& f, int pt) {
 #pragma unroll
   for (int it = 0; it < 4; ++it) {
     const int c = (pt >> 4) + 16 * it, sg = pt & 15;
@@ -808,18 +834,13 @@ __device__ __forceinline__ void stage_kq_gates(const ChunkBufs& cb, const Produc
     *reinterpret_cast<uint2*>(cb.Q + pa) = uint2{f.q[it].x, f.q[it].y};
     *reinterpret_cast<uint2*>(cb.Q + pb) = uint2{f.q[it].z, f.q[it].w};
   }
-  if (pw == 0) {
-    const float lg = lane < clen ? fast_log2_gate(neg_decay, bf16_to_f32(f.a) + dt_bias) : 0.f;
-    const float bt = lane < clen ? fast_sigmoid(bf16_to_f32(f.b)) : 0.f;
-    float gml;
-    const float gm = wave_inclusive_scan2(lg, gml);
-    const float glast = readlane_f(gm, clen - 1), glastl = readlane_f(gml, clen - 1);
-    cb.gam[lane] = gm;
-    cb.gaml[lane] = gml;
-    cb.bet[lane] = bt;
-    cb.eg[lane] = exp2_le0(gm);
-    cb.dd[lane] = exp2_le0(fminf(gamma_diff(glast, glastl, gm, gml), 0.f));
-  }
+}
+
+// Step 1 with the chunk's gates formed in place (first wave).
+__device__ __forceinline__ void stage_kq_gates(const ChunkBufs& cb, const ProducerPrefetch& f, int pt, int pw, int lane,
+                                               int clen, float neg_decay, float dt_bias) {
+  stage_kq(cb, f, pt);
+  if (pw == 0) store_gates(cb, chunk_gates(f, lane, clen, neg_decay, dt_bias), lane);
 }
 
 // Producer thread pt's share of a chunk's T~ hi, T~ lo and P tiles (their LDS
@@ -863,6 +884,10 @@ __device__ __forceinline__ void producer_loop(Smem& sm, const PrefillArgs& p, in
   ProducerPrefetch f;
   uint4 fv[NVIT];
   producer_prefetch(p, s0, int(s1 - s0 < C ? s1 - s0 : C), h, hq, hk, pt, lo, f);
+  // The first wave forms each chunk's gates one tick ahead (chunk t + 1's in step 3
+  // of tick t, where it has slack) and stores them with the chunk's K and Q.
+  ChunkGates gts = {0.f, 0.f, 0.f, 0.f, 0.f};
+  if (pw == 0) gts = chunk_gates(f, lane0, int(s1 - s0 < C ? s1 - s0 : C), neg_decay, dt_bias);
   PhaseClock clk;
   clk.start();
 
@@ -888,7 +913,8 @@ __device__ __forceinline__ void producer_loop(Smem& sm, const PrefillArgs& p, in
     clk.lap(0);
 
     // 1: stage K/Q (permuted columns), gates
-    stage_kq_gates(cb, f, pt, pw, lane, clen, neg_decay, dt_bias);
+    stage_kq(cb, f, pt);
+    if (pw == 0) store_gates(cb, gts, lane);
     // The V slice of this chunk into registers; staged at the end of the tick,
     // after the consumers' last read of the previous chunk's V.
     {
@@ -970,6 +996,7 @@ __device__ __forceinline__ void producer_loop(Smem& sm, const PrefillArgs& p, in
         if (kSolveFirst && ncs < s1) producer_prefetch(p, ncs, nclen, h, hq, hk, pt, lo, f);
         const TileJob j1[2] = {{2, 2, 1}, {2, 2, 2}};
         run_tiles(sm, cb, j1, p.scale, lane);
+        if (ncs < s1) gts = chunk_gates(f, lane, nclen, neg_decay, dt_bias);  // chunk t + 1's gates
         break;
       }
       case 1: {
