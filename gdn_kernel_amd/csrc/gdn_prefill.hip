@@ -80,26 +80,40 @@ constexpr int TSTR = 72;     // bf16 row stride of 64-wide tiles (T~, P, N)
 constexpr int NDB = 16 * 16 + 4;  // floats per diagonal N block (column-major; padded by 16 bytes)
 constexpr int NROWS = C - 16;  // rows of N kept for the off-diagonal solve
 
-template <int NCW_, int VT_, bool HOOKS_ = false, bool LOAD_ = false>
+template <int NCW_, int VT_, bool HOOKS_ = false, bool LOAD_ = false, int NP_ = 4>
 struct Variant {
   static constexpr bool kHooks = HOOKS_;         // testing hooks of PrefillArgs compiled in
   static constexpr bool kLoad = LOAD_;           // waves NCW.. load prepared T~/P (two-kernel path)
   static constexpr bool kCopy = false;           // producers copy their tiles out (prep kernel only)
   static constexpr int NCW = NCW_;               // consumer waves
+  static constexpr int NP = NP_;                 // producer (or loader) waves: 4, or 7 beside one consumer
   static constexpr int VT = VT_;                 // 16-row state tiles per consumer wave
   static constexpr int VW = 16 * VT;             // state rows per consumer wave
   static constexpr int ROWS = NCW * VW;          // state rows per workgroup
   static constexpr int F = 128 / ROWS;           // workgroups per chain
-  static constexpr int NTHREADS = 64 * (NCW + 4);
+  static constexpr int NTHREADS = 64 * (NCW + NP);
   static constexpr int VSEG = 8 * ROWS;          // 16-byte segments of the V slice of a chunk
-  static_assert(F * ROWS == 128 && NCW + 4 <= 8, "unsupported launch variant");
+  static_assert(F * ROWS == 128 && NCW + NP <= 8, "unsupported launch variant");
+  static_assert(NP == 4 || (NP == 7 && NCW == 1 && !LOAD_), "seven producers only beside one consumer");
 };
+
+// Production launch variants by split factor F (workgroups per chain).  With F = 8 a
+// chain's slice has one 16-row consumer wave and the chunk preparation, repeated in
+// every slice, sets the pace: seven producer waves share it.
+template <bool HOOKS>
+using SplitVariant1 = Variant<4, 2, HOOKS>;
+template <bool HOOKS>
+using SplitVariant2 = Variant<4, 1, HOOKS>;
+template <bool HOOKS>
+using SplitVariant4 = Variant<2, 1, HOOKS>;
+template <bool HOOKS>
+using SplitVariant8 = Variant<1, 1, HOOKS, false, 7>;
 
 // The prep kernel of the two-kernel path: the four producer waves alone (no
 // consumers, no V staging); they copy each chunk's tiles out themselves (kCopy).
 struct PrepVariant {
   static constexpr bool kHooks = false, kLoad = false, kCopy = true;
-  static constexpr int NCW = 0, VT = 1, VW = 16, ROWS = 128, F = 1;
+  static constexpr int NCW = 0, NP = 4, VT = 1, VW = 16, ROWS = 128, F = 1;
   static constexpr int NTHREADS = 64 * (NCW + 4);
   static constexpr int VSEG = 0;
 };
@@ -881,9 +895,12 @@ __device__ __forceinline__ void producer_loop(Smem& sm, const PrefillArgs& p, in
     vrow[it] = seg < V::VSEG ? c : C;  // C: no segment
     voff[it] = c * p.Hv * D + 8 * sg;
   }
-  ProducerPrefetch f;
+  // With seven producer waves, the first four stage K, Q and V and issue their loads
+  // (256 threads, as with four); the other three only compute tiles.
+  const bool stager = V::NP == 4 || pw < 4;
+  ProducerPrefetch f = {};
   uint4 fv[NVIT];
-  producer_prefetch(p, s0, int(s1 - s0 < C ? s1 - s0 : C), h, hq, hk, pt, lo, f);
+  if (stager) producer_prefetch(p, s0, int(s1 - s0 < C ? s1 - s0 : C), h, hq, hk, pt, lo, f);
   // The first wave forms each chunk's gates one tick ahead (chunk t + 1's in step 3
   // of tick t, where it has slack) and stores them with the chunk's K and Q.
   ChunkGates gts = {0.f, 0.f, 0.f, 0.f, 0.f};
@@ -913,11 +930,11 @@ __device__ __forceinline__ void producer_loop(Smem& sm, const PrefillArgs& p, in
     clk.lap(0);
 
     // 1: stage K/Q (permuted columns), gates
-    stage_kq(cb, f, pt);
+    if (stager) stage_kq(cb, f, pt);
     if (pw == 0) store_gates(cb, gts, lane);
     // The V slice of this chunk into registers; staged at the end of the tick,
     // after the consumers' last read of the previous chunk's V.
-    {
+    if (stager) {
       const uint16_t* vb = p.v + (cs * p.Hv + h) * D + row0;
 #pragma unroll
       for (int it = 0; it < NVIT; ++it) {
@@ -927,7 +944,7 @@ __device__ __forceinline__ void producer_loop(Smem& sm, const PrefillArgs& p, in
     }
     clk.lap(1);
     signal_count(sm, kPPhase, lane);
-    wait_count<V::kHooks>(sm, kPPhase, 4 * (2 * t + 1));  // all of K/Q/gates staged
+    wait_count<V::kHooks>(sm, kPPhase, V::NP * (2 * t + 1));  // all of K/Q/gates staged
     clk.lap(2);
     // The rest of the chunk is the longer chain: producer waves go ahead of the
     // consumer wave sharing the SIMD.
@@ -943,6 +960,65 @@ __device__ __forceinline__ void producer_loop(Smem& sm, const PrefillArgs& p, in
     constexpr bool kSolveFirst = V::F > 1;
     if (!kSolveFirst && ncs < s1) producer_prefetch(p, ncs, nclen, h, hq, hk, pt, lo, f);
     clk.lap(10);
+    if constexpr (V::NP == 7) {
+      // Seven waves: the solve wave only solves (its loads go first, under its wait
+      // for the diagonal tiles), four waves form the diagonal tiles and the six
+      // off-diagonal N tiles (or two P tiles), two waves form the other P tiles.
+      switch (pw) {
+        case 0:
+          if (ncs < s1) producer_prefetch(p, ncs, nclen, h, hq, hk, pt, lo, f);
+          wait_count<V::kHooks>(sm, kDiagN, 4 * (t + 1));
+          clk.lap(4);
+          diag_solve(sm, cb, lane);
+          clk.lap(5);
+          break;
+        case 1: {
+          diag_tiles<1, 2>(sm, cb, lane);
+          signal_count(sm, kDiagN, lane);
+          if (ncs < s1) producer_prefetch(p, ncs, nclen, h, hq, hk, pt, lo, f);
+          const TileJob j1[2] = {{1, 1, 0}, {1, 2, 0}};
+          run_tiles(sm, cb, j1, p.scale, lane);
+          break;
+        }
+        case 2: {
+          diag_tiles<2, 3>(sm, cb, lane);
+          signal_count(sm, kDiagN, lane);
+          if (ncs < s1) producer_prefetch(p, ncs, nclen, h, hq, hk, pt, lo, f);
+          const TileJob j1[2] = {{1, 3, 0}, {1, 2, 1}};
+          run_tiles(sm, cb, j1, p.scale, lane);
+          break;
+        }
+        case 3: {
+          diag_tiles<3, 4>(sm, cb, lane);
+          signal_count(sm, kDiagN, lane);
+          if (ncs < s1) producer_prefetch(p, ncs, nclen, h, hq, hk, pt, lo, f);
+          const TileJob j1[2] = {{1, 3, 1}, {1, 3, 2}};
+          run_tiles(sm, cb, j1, p.scale, lane);
+          break;
+        }
+        case 4: {
+          diag_tiles<0, 1>(sm, cb, lane);
+          signal_count(sm, kDiagN, lane);
+          const TileJob j1[2] = {{2, 0, 0}, {2, 3, 3}};
+          run_tiles(sm, cb, j1, p.scale, lane);
+          break;
+        }
+        case 5: {
+          const TileJob j1[2] = {{2, 1, 0}, {2, 3, 0}};
+          run_tiles(sm, cb, j1, p.scale, lane);
+          const TileJob j2[2] = {{2, 1, 1}, {2, 2, 0}};
+          run_tiles(sm, cb, j2, p.scale, lane);
+          break;
+        }
+        default: {
+          const TileJob j1[2] = {{2, 2, 1}, {2, 2, 2}};
+          run_tiles(sm, cb, j1, p.scale, lane);
+          const TileJob j2[2] = {{2, 3, 1}, {2, 3, 2}};
+          run_tiles(sm, cb, j2, p.scale, lane);
+          break;
+        }
+      }
+    } else {
     switch (pw) {
       case 0:
         diag_tiles<0, 1>(sm, cb, lane);
@@ -984,13 +1060,29 @@ __device__ __forceinline__ void producer_loop(Smem& sm, const PrefillArgs& p, in
         break;
       }
     }
+    }
     clk.lap(3);
     signal_count(sm, kPPhase, lane);
-    wait_count<V::kHooks>(sm, kPPhase, 4 * (2 * t + 2));  // diagonal blocks and N tiles done
+    wait_count<V::kHooks>(sm, kPPhase, V::NP * (2 * t + 2));  // diagonal blocks and N tiles done
     clk.lap(6);
 
     // 3: off-diagonal blocks of T~ (waves 1 and 3), the remaining P tiles (two
     // each on waves 0 and 2), V once the consumers have read the previous chunk's
+    if constexpr (V::NP == 7) {
+      switch (pw) {
+        case 0:
+          if (ncs < s1) gts = chunk_gates(f, lane, nclen, neg_decay, dt_bias);  // chunk t + 1's gates
+          break;
+        case 1:
+          offdiag_right(sm, cb, t, lane);
+          break;
+        case 3:
+          offdiag_left<V::kHooks>(sm, cb, t, lane);
+          break;
+        default:
+          break;
+      }
+    } else {
     switch (pw) {
       case 0: {
         if (kSolveFirst && ncs < s1) producer_prefetch(p, ncs, nclen, h, hq, hk, pt, lo, f);
@@ -1012,17 +1104,20 @@ __device__ __forceinline__ void producer_loop(Smem& sm, const PrefillArgs& p, in
         offdiag_left<V::kHooks>(sm, cb, t, lane);
         break;
     }
+    }
     clk.lap(7);
-    if (t >= 1) wait_count<V::kHooks>(sm, kVFree, V::NCW * t);
-    clk.lap(8);
+    if (stager) {  // the staging waves stage V and hand the chunk over (four signals a chunk)
+      if (t >= 1) wait_count<V::kHooks>(sm, kVFree, V::NCW * t);
+      clk.lap(8);
 #pragma unroll
-    for (int it = 0; it < NVIT; ++it) {
-      const int seg = pt + it * NPROD;
-      if (seg < V::VSEG)
-        *reinterpret_cast<uint4*>(sm.V + (seg / (V::ROWS / 8)) * VSTR + 8 * (seg % (V::ROWS / 8))) = fv[it];
+      for (int it = 0; it < NVIT; ++it) {
+        const int seg = pt + it * NPROD;
+        if (seg < V::VSEG)
+          *reinterpret_cast<uint4*>(sm.V + (seg / (V::ROWS / 8)) * VSTR + 8 * (seg % (V::ROWS / 8))) = fv[it];
+      }
     }
     __builtin_amdgcn_s_setprio(0);
-    if (!V::kHooks || p.ready_chunks <= 0 || t < p.ready_chunks) signal_count(sm, kReady, lane);
+    if (stager && (!V::kHooks || p.ready_chunks <= 0 || t < p.ready_chunks)) signal_count(sm, kReady, lane);
     clk.lap(9);
   }
   if constexpr (V::kCopy) {
@@ -1357,7 +1452,12 @@ __global__ __launch_bounds__(V::NTHREADS) void gdn_prefill_kernel(PrefillArgs p)
   // and two (mostly idle) loaders share SIMD 0: config 3 174 -> 170 us.  Elsewhere
   // the natural order measured as fast or faster (two consumers on SIMDs of their
   // own: +1.5%; the producer variant's solve wave sharing a SIMD: +7%).
-  const int wave = !(V::kLoad && NCW == 1) ? hw : hw == 3 ? 0 : hw < 3 ? hw + 1 : hw;
+  // With seven producers (beside one consumer) the consumer keeps hardware wave 0 and
+  // shares its SIMD with the producer that has least to do (P tiles in step 2 only):
+  // hardware waves 1-7 take producers 0, 1, 3, 6, 4, 2, 5.
+  const int wave = V::NP == 7 ? (hw == 0 ? 0 : 1 + ((0x5246310 >> (4 * (hw - 1))) & 15))
+                   : !(V::kLoad && NCW == 1) ? hw
+                   : hw == 3 ? 0 : hw < 3 ? hw + 1 : hw;
 
   const int bid = blockIdx.x;
   // F == 1: blocks b and b + 8 of each group of 16 take chains 2m and 2m + 1 (v-heads
@@ -1607,10 +1707,10 @@ int64_t prefill_work_items(int64_t chains) {
   const int F = split_factor(chains);
   const int64_t grid = F == 1 ? (chains + 15) / 16 * 16 : (chains + 7) / 8 * 8 * F;
   switch (F) {
-    case 1: return grid * Variant<4, 2>::NTHREADS;
-    case 2: return grid * Variant<4, 1>::NTHREADS;
-    case 4: return grid * Variant<2, 1>::NTHREADS;
-    default: return grid * Variant<1, 1>::NTHREADS;
+    case 1: return grid * SplitVariant1<false>::NTHREADS;
+    case 2: return grid * SplitVariant2<false>::NTHREADS;
+    case 4: return grid * SplitVariant4<false>::NTHREADS;
+    default: return grid * SplitVariant8<false>::NTHREADS;
   }
 }
 
@@ -1639,10 +1739,10 @@ hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream) {
   // production launches keep them out of the device code.
   if (a.spin_limit != 0 || a.ready_chunks != 0 || a.aborts != nullptr) {
     switch (F) {
-      case 1: return launch_variant<Variant<4, 2, true>>(a, stream);
-      case 2: return launch_variant<Variant<4, 1, true>>(a, stream);
-      case 4: return launch_variant<Variant<2, 1, true>>(a, stream);
-      default: return launch_variant<Variant<1, 1, true>>(a, stream);
+      case 1: return launch_variant<SplitVariant1<true>>(a, stream);
+      case 2: return launch_variant<SplitVariant2<true>>(a, stream);
+      case 4: return launch_variant<SplitVariant4<true>>(a, stream);
+      default: return launch_variant<SplitVariant8<true>>(a, stream);
     }
   }
   if (a.tiles != nullptr && prefill_workspace_bytes(a.N, a.T, a.Hv) > 0) {
@@ -1665,10 +1765,10 @@ hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream) {
   // shorter than a 32-row wave's.  Unsplit chains (F = 1) keep four 32-row waves:
   // eight 16-row waves and the four producers would exceed the register file.
   switch (F) {
-    case 1: return launch_variant<Variant<4, 2>>(a, stream);
-    case 2: return launch_variant<Variant<4, 1>>(a, stream);
-    case 4: return launch_variant<Variant<2, 1>>(a, stream);
-    default: return launch_variant<Variant<1, 1>>(a, stream);
+    case 1: return launch_variant<SplitVariant1<false>>(a, stream);
+    case 2: return launch_variant<SplitVariant2<false>>(a, stream);
+    case 4: return launch_variant<SplitVariant4<false>>(a, stream);
+    default: return launch_variant<SplitVariant8<false>>(a, stream);
   }
 }
 
