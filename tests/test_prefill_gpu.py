@@ -393,7 +393,8 @@ def test_prefill_workspace_reuse(gpu):
 
 
 @pytest.mark.giveups_expected
-def test_prefill_bounded_waits(gpu):
+@pytest.mark.parametrize("heads,split", [(Heads(16, 16, 32), 2), (Heads(4, 4, 8), 8)])
+def test_prefill_bounded_waits(gpu, heads, split):
     """The hand-off failure path, forced from the host.  With the testing hooks off
     the entry point is gdn_prefill bit for bit and nothing gives up.  With the
     producers signalling only their first chunk and a 2,000-poll wait limit, every
@@ -402,9 +403,10 @@ def test_prefill_bounded_waits(gpu):
     counted both by the hook counter and by the device counter that
     gdn_prefill_giveups reports, every output and final-state element of the affected
     sequences is NaN, the one-chunk sequence's results are untouched, and the next
-    normal launch is exact again."""
-    lens = [300, 130, 40]             # 5, 3 and 1 chunks; 96 chains: split 2 ways
-    p = workloads.prefill_inputs(lens, seed=21, gate="slow", state_scale=0.5)
+    normal launch is exact again.  With 32 v-heads the 96 chains split 2 ways (four
+    producer waves per workgroup); with 8 the 24 chains split 8 ways (seven)."""
+    lens = [300, 130, 40]             # 5, 3 and 1 chunks
+    p = workloads.prefill_inputs(lens, heads, seed=21, gate="slow", state_scale=0.5)
     binding.prefill_giveups(reset=True)
     say("prefill bounded waits: hooks off")
     o0, s0, a0 = _prefill_fault_injection(p, gpu, 0, 0)
@@ -415,7 +417,7 @@ def test_prefill_bounded_waits(gpu):
     say("prefill bounded waits: chunk-ready signals stop after chunk 0, 2000-poll limit")
     o2, s2, a2 = _prefill_fault_injection(p, gpu, 2000, 1)
     torch.cuda.synchronize()
-    waiting_wgs = 2 * 32 * 2          # sequences with >= 2 chunks x v-heads x workgroups per chain
+    waiting_wgs = 2 * heads.hv * split  # sequences with >= 2 chunks x v-heads x workgroups per chain
     n = int(a2.item())
     assert waiting_wgs <= n <= waiting_wgs * 8, n
     assert binding.prefill_giveups(reset=True) == n, "the device counter must see every give-up"
