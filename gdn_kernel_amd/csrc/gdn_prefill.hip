@@ -2,9 +2,10 @@
 //
 // A workgroup walks the chunks of one (sequence, v-head) chain, or of one slice
 // of its state rows, as a two-stage pipeline:
-//   * four producer waves (NCW .. NCW+3) prepare chunk t: stage K and Q in LDS,
-//     form the gates, the masked/decayed products N = strictLower(beta Gamma KK^T)
-//     and P = tril(Gamma QK^T), and T~ = (I + N)^-1;
+//   * NP producer waves (NCW .. NCW+NP-1; four, or seven beside a single consumer)
+//     prepare chunk t: stage K and Q in LDS, form the gates, the masked/decayed
+//     products N = strictLower(beta Gamma KK^T) and P = tril(Gamma QK^T), and
+//     T~ = (I + N)^-1;
 //   * the consumer waves (0 .. NCW-1) meanwhile advance the state through chunk t-1.
 // Every LDS buffer a consumer reads (K, Q, T~, P, gates) is double-buffered by
 // chunk parity (V is single-buffered and rewritten only after it was read).
@@ -19,7 +20,9 @@
 // each owning rows [R0, R0 + ROWS).  They all prepare the same chunk data (the
 // producer work does not depend on the state) and each stages only its slice of
 // V.  Batches with many chains use F = 1 (four consumer waves of 32 rows); few
-// chains are split so that every CU gets a workgroup.  When the caller provides
+// chains are split so that every CU gets a workgroup (with F = 8 one 16-row
+// consumer and seven producers, whose repeated chunk preparation sets the pace).
+// When the caller provides
 // a workspace, batches split 4 or 8 ways run in two kernels instead: a prep kernel
 // prepares every chunk once (all chunks in parallel), and the state pass's loader
 // waves copy its T~/P tiles where the producers would have computed them.
