@@ -145,7 +145,7 @@ struct __align__(16) PrefillSmem {
   float eg[2][C];             // e^{gamma_c}
   float dd[2][C];             // e^{gamma_last - gamma_c}
   int seq;                    // sequence handled by this workgroup
-  int sync[8];                // hand-off counters (kReady, kVFree, kConsumed, kPPhase, kAbort, kDiagN, kX32)
+  int sync[16];               // hand-off counters (enum SyncCounter)
   int spin_limit;             // kernels with testing hooks: polls before a hand-off wait gives up
   unsigned* aborts;           // kernels with testing hooks: optional count of waits that gave up
 };
@@ -169,7 +169,7 @@ struct __align__(16) PrepSmem {
   float bet[1][C];
   float eg[1][C];
   float dd[1][C];
-  int sync[8];
+  int sync[16];
   int spin_limit;
   unsigned* aborts;
 };
@@ -395,7 +395,18 @@ namespace {
 // Hand-off between the two roles: monotonically increasing LDS counters.  A wave
 // signals by adding 1 after all its earlier LDS accesses completed (release); a
 // waiter polls until the count reaches its target (acquire).
-enum SyncCounter { kReady = 0, kVFree = 1, kConsumed = 2, kPPhase = 3, kAbort = 4, kDiagN = 5, kX32 = 6 };
+enum SyncCounter {
+  kReady = 0,     // chunk handed over to the consumers (4 a chunk; seven producers: its T~ and P, 6)
+  kVFree = 1,     // consumers read the chunk's V
+  kConsumed = 2,  // consumers done with the chunk's buffers
+  kPPhase = 3,    // four producers: their step barriers; seven: solve and N tiles done (3 a chunk)
+  kAbort = 4,     // a wait gave up
+  kDiagN = 5,     // diagonal N tiles formed (4 a chunk)
+  kX32 = 6,       // off-diagonal block X32 stored
+  kStaged = 7,    // seven producers: the chunk's K/Q staged and its gates stored (5 a chunk)
+  kNRead = 8,     // seven producers: the left off-diagonal wave read its N operands
+  kVStaged = 9    // seven producers: the chunk's V staged (4 a chunk)
+};
 constexpr int kSpinLimit = 1 << 21;  // default polls (about 70 ms) before a wait gives up
 
 template <class Smem>
@@ -746,7 +757,7 @@ __device__ __forceinline__ void offdiag_right(Smem& sm, const ChunkBufs& cb, int
   (void)t;
 }
 
-template <bool kHooks, class Smem>
+template <bool kHooks, bool kSignalNRead = false, class Smem>
 __device__ __forceinline__ void offdiag_left(Smem& sm, const ChunkBufs& cb, int t, int lane) {
   const Pair2 d0 = diag_b(cb, 0, lane);
   const Pair2 a1 = block_a(cb.Th, cb.Tl, 0, 1, 1, lane), a2 = block_a(cb.Th, cb.Tl, 0, 2, 2, lane),
@@ -754,6 +765,9 @@ __device__ __forceinline__ void offdiag_left(Smem& sm, const ChunkBufs& cb, int 
   const Pair2 n10 = block_a(sm.Nh, sm.Nl, 16, 1, 0, lane), n20 = block_a(sm.Nh, sm.Nl, 16, 2, 0, lane),
               n21 = block_a(sm.Nh, sm.Nl, 16, 2, 1, lane), n30 = block_a(sm.Nh, sm.Nl, 16, 3, 0, lane),
               n31 = block_a(sm.Nh, sm.Nl, 16, 3, 1, lane);
+  // (Seven producers: the N tiles of the next chunk may be written once these reads
+  // are done; the signal's release waits for them.)
+  if constexpr (kSignalNRead) signal_count(sm, kNRead, lane);
   const f32x4 g10 = mul3_16(zero4(), n10, d0);
   const f32x4 p20 = mul3_16(zero4(), n20, d0);
   const f32x4 p30 = mul3_16(zero4(), n30, d0);
@@ -898,12 +912,10 @@ __device__ __forceinline__ void producer_loop(Smem& sm, const PrefillArgs& p, in
     vrow[it] = seg < V::VSEG ? c : C;  // C: no segment
     voff[it] = c * p.Hv * D + 8 * sg;
   }
-  // With seven producer waves, the first four stage K, Q and V and issue their loads
-  // (256 threads, as with four); the other three only compute tiles.
-  const bool stager = V::NP == 4 || pw < 4;
-  ProducerPrefetch f = {};
+  static_assert(V::NP == 4, "seven producer waves run producer_loop7");
+  ProducerPrefetch f;
   uint4 fv[NVIT];
-  if (stager) producer_prefetch(p, s0, int(s1 - s0 < C ? s1 - s0 : C), h, hq, hk, pt, lo, f);
+  producer_prefetch(p, s0, int(s1 - s0 < C ? s1 - s0 : C), h, hq, hk, pt, lo, f);
   // The first wave forms each chunk's gates one tick ahead (chunk t + 1's in step 3
   // of tick t, where it has slack) and stores them with the chunk's K and Q.
   ChunkGates gts = {0.f, 0.f, 0.f, 0.f, 0.f};
@@ -933,11 +945,11 @@ __device__ __forceinline__ void producer_loop(Smem& sm, const PrefillArgs& p, in
     clk.lap(0);
 
     // 1: stage K/Q (permuted columns), gates
-    if (stager) stage_kq(cb, f, pt);
+    stage_kq(cb, f, pt);
     if (pw == 0) store_gates(cb, gts, lane);
     // The V slice of this chunk into registers; staged at the end of the tick,
     // after the consumers' last read of the previous chunk's V.
-    if (stager) {
+    {
       const uint16_t* vb = p.v + (cs * p.Hv + h) * D + row0;
 #pragma unroll
       for (int it = 0; it < NVIT; ++it) {
@@ -947,7 +959,7 @@ __device__ __forceinline__ void producer_loop(Smem& sm, const PrefillArgs& p, in
     }
     clk.lap(1);
     signal_count(sm, kPPhase, lane);
-    wait_count<V::kHooks>(sm, kPPhase, V::NP * (2 * t + 1));  // all of K/Q/gates staged
+    wait_count<V::kHooks>(sm, kPPhase, 4 * (2 * t + 1));  // all of K/Q/gates staged
     clk.lap(2);
     // The rest of the chunk is the longer chain: producer waves go ahead of the
     // consumer wave sharing the SIMD.
@@ -963,65 +975,6 @@ __device__ __forceinline__ void producer_loop(Smem& sm, const PrefillArgs& p, in
     constexpr bool kSolveFirst = V::F > 1;
     if (!kSolveFirst && ncs < s1) producer_prefetch(p, ncs, nclen, h, hq, hk, pt, lo, f);
     clk.lap(10);
-    if constexpr (V::NP == 7) {
-      // Seven waves: the solve wave only solves (its loads go first, under its wait
-      // for the diagonal tiles), four waves form the diagonal tiles and the six
-      // off-diagonal N tiles (or two P tiles), two waves form the other P tiles.
-      switch (pw) {
-        case 0:
-          if (ncs < s1) producer_prefetch(p, ncs, nclen, h, hq, hk, pt, lo, f);
-          wait_count<V::kHooks>(sm, kDiagN, 4 * (t + 1));
-          clk.lap(4);
-          diag_solve(sm, cb, lane);
-          clk.lap(5);
-          break;
-        case 1: {
-          diag_tiles<1, 2>(sm, cb, lane);
-          signal_count(sm, kDiagN, lane);
-          if (ncs < s1) producer_prefetch(p, ncs, nclen, h, hq, hk, pt, lo, f);
-          const TileJob j1[2] = {{1, 1, 0}, {1, 2, 0}};
-          run_tiles(sm, cb, j1, p.scale, lane);
-          break;
-        }
-        case 2: {
-          diag_tiles<2, 3>(sm, cb, lane);
-          signal_count(sm, kDiagN, lane);
-          if (ncs < s1) producer_prefetch(p, ncs, nclen, h, hq, hk, pt, lo, f);
-          const TileJob j1[2] = {{1, 3, 0}, {1, 2, 1}};
-          run_tiles(sm, cb, j1, p.scale, lane);
-          break;
-        }
-        case 3: {
-          diag_tiles<3, 4>(sm, cb, lane);
-          signal_count(sm, kDiagN, lane);
-          if (ncs < s1) producer_prefetch(p, ncs, nclen, h, hq, hk, pt, lo, f);
-          const TileJob j1[2] = {{1, 3, 1}, {1, 3, 2}};
-          run_tiles(sm, cb, j1, p.scale, lane);
-          break;
-        }
-        case 4: {
-          diag_tiles<0, 1>(sm, cb, lane);
-          signal_count(sm, kDiagN, lane);
-          const TileJob j1[2] = {{2, 0, 0}, {2, 3, 3}};
-          run_tiles(sm, cb, j1, p.scale, lane);
-          break;
-        }
-        case 5: {
-          const TileJob j1[2] = {{2, 1, 0}, {2, 3, 0}};
-          run_tiles(sm, cb, j1, p.scale, lane);
-          const TileJob j2[2] = {{2, 1, 1}, {2, 2, 0}};
-          run_tiles(sm, cb, j2, p.scale, lane);
-          break;
-        }
-        default: {
-          const TileJob j1[2] = {{2, 2, 1}, {2, 2, 2}};
-          run_tiles(sm, cb, j1, p.scale, lane);
-          const TileJob j2[2] = {{2, 3, 1}, {2, 3, 2}};
-          run_tiles(sm, cb, j2, p.scale, lane);
-          break;
-        }
-      }
-    } else {
     switch (pw) {
       case 0:
         diag_tiles<0, 1>(sm, cb, lane);
@@ -1063,29 +1016,13 @@ __device__ __forceinline__ void producer_loop(Smem& sm, const PrefillArgs& p, in
         break;
       }
     }
-    }
     clk.lap(3);
     signal_count(sm, kPPhase, lane);
-    wait_count<V::kHooks>(sm, kPPhase, V::NP * (2 * t + 2));  // diagonal blocks and N tiles done
+    wait_count<V::kHooks>(sm, kPPhase, 4 * (2 * t + 2));  // diagonal blocks and N tiles done
     clk.lap(6);
 
     // 3: off-diagonal blocks of T~ (waves 1 and 3), the remaining P tiles (two
     // each on waves 0 and 2), V once the consumers have read the previous chunk's
-    if constexpr (V::NP == 7) {
-      switch (pw) {
-        case 0:
-          if (ncs < s1) gts = chunk_gates(f, lane, nclen, neg_decay, dt_bias);  // chunk t + 1's gates
-          break;
-        case 1:
-          offdiag_right(sm, cb, t, lane);
-          break;
-        case 3:
-          offdiag_left<V::kHooks>(sm, cb, t, lane);
-          break;
-        default:
-          break;
-      }
-    } else {
     switch (pw) {
       case 0: {
         if (kSolveFirst && ncs < s1) producer_prefetch(p, ncs, nclen, h, hq, hk, pt, lo, f);
@@ -1107,26 +1044,220 @@ __device__ __forceinline__ void producer_loop(Smem& sm, const PrefillArgs& p, in
         offdiag_left<V::kHooks>(sm, cb, t, lane);
         break;
     }
-    }
     clk.lap(7);
-    if (stager) {  // the staging waves stage V and hand the chunk over (four signals a chunk)
-      if (t >= 1) wait_count<V::kHooks>(sm, kVFree, V::NCW * t);
-      clk.lap(8);
+    if (t >= 1) wait_count<V::kHooks>(sm, kVFree, V::NCW * t);
+    clk.lap(8);
 #pragma unroll
-      for (int it = 0; it < NVIT; ++it) {
-        const int seg = pt + it * NPROD;
-        if (seg < V::VSEG)
-          *reinterpret_cast<uint4*>(sm.V + (seg / (V::ROWS / 8)) * VSTR + 8 * (seg % (V::ROWS / 8))) = fv[it];
-      }
+    for (int it = 0; it < NVIT; ++it) {
+      const int seg = pt + it * NPROD;
+      if (seg < V::VSEG)
+        *reinterpret_cast<uint4*>(sm.V + (seg / (V::ROWS / 8)) * VSTR + 8 * (seg % (V::ROWS / 8))) = fv[it];
     }
     __builtin_amdgcn_s_setprio(0);
-    if (stager && (!V::kHooks || p.ready_chunks <= 0 || t < p.ready_chunks)) signal_count(sm, kReady, lane);
+    if (!V::kHooks || p.ready_chunks <= 0 || t < p.ready_chunks) signal_count(sm, kReady, lane);
     clk.lap(9);
   }
   if constexpr (V::kCopy) {
     wait_count<V::kHooks>(sm, kReady, 4 * nchunks);
     copy_tiles_out(chunk_bufs(sm, (nchunks - 1) & 1), images + int64_t(nchunks - 1) * p.Hv * kTileImage, pt,
                    aborted(sm));
+  }
+  clk.store(V::NCW + pw, lane0);
+}
+
+// The raw gate inputs (a, b) of token `lane` of a chunk, clamped into the chunk.
+__device__ __forceinline__ void prefetch_gate_inputs(const PrefillArgs& p, int64_t cs, int clen, int h, int lane,
+                                                     ProducerPrefetch& f) {
+  const int off = (lane < clen ? lane : clen - 1) * p.Hv;
+  f.a = (p.a + cs * p.Hv + h)[off];
+  f.b = (p.b + cs * p.Hv + h)[off];
+}
+
+template <int SI, class Smem>
+__device__ __forceinline__ void diag_tile_of(Smem& sm, const ChunkBufs& cb, int lane) {
+  diag_tiles<SI, SI + 1>(sm, cb, lane);
+}
+
+// The producer loop with seven waves beside one consumer (chains split 8 ways),
+// pipelined one step deep.  For chunk t:
+//   * wave 0 solves the diagonal blocks of T~ once chunk t's four diagonal N tiles
+//     are in, then forms chunk t + 1's gates;
+//   * waves 1 and 3 form the six off-diagonal N tiles (and one P tile each), then
+//     the off-diagonal blocks of T~ (offdiag_right, offdiag_left);
+//   * the stager waves 2, 4, 5 and 6 form the other eight P tiles and stage V, then
+//     stage chunk t + 1's K and Q and form its four diagonal N tiles,
+// so the solve of chunk t + 1 can start as soon as chunk t's is done, instead of
+// after chunk t + 1's staging and diagonal tiles.  Hand-offs per chunk: kStaged 5
+// (the stagers' K/Q and wave 0's gates), kDiagN 4, kPPhase 3 (the solve, and the N
+// tiles of waves 1 and 3), kNRead 1 (the left off-diagonal wave read its N operands,
+// so the next chunk's N tiles may overwrite them), kX32 1, kReady 6 (waves 1 and
+// 3, the stagers).  Every buffer of chunk t + 1's parity is written only after the
+// consumers signalled chunk t - 1 consumed.
+template <class V>
+__device__ __forceinline__ void producer_loop7(PrefillSmem& sm, const PrefillArgs& p, int64_t s0, int64_t s1,
+                                               int nchunks, int h, int hq, int hk, int row0, int pw, int lane0) {
+  static_assert(V::NP == 7 && V::NCW == 1 && !V::kLoad && !V::kCopy, "seven-producer loop");
+  constexpr int NVIT = (V::VSEG + NPROD - 1) / NPROD;  // V segments per stager thread
+  const int si = pw == 2 ? 0 : pw >= 4 ? pw - 3 : -1;   // stager index (waves 2, 4, 5, 6)
+  const int pt = (si < 0 ? 0 : si) * 64 + lane0;        // thread index among the stagers
+  const float neg_decay = -expf(p.A_log[h]);
+  const float dt_bias = p.dt_bias[h];
+  const LaneOffsets lo = {(pt >> 4) * p.Hk * D + 8 * (pt & 15), (pt >> 4) * p.Hq * D + 8 * (pt & 15), pt * p.Hv};
+  int voff[NVIT], vrow[NVIT];
+#pragma unroll
+  for (int it = 0; it < NVIT; ++it) {
+    const int seg = pt + it * NPROD, c = seg / (V::ROWS / 8), sg = seg % (V::ROWS / 8);
+    vrow[it] = seg < V::VSEG ? c : C;  // C: no segment
+    voff[it] = c * p.Hv * D + 8 * sg;
+  }
+  auto chunk_len = [&](int64_t cs) { return int(s1 - cs < C ? s1 - cs : C); };
+  auto load_v = [&](uint4 (&fv)[NVIT], int64_t cs) {
+    const uint16_t* vb = p.v + (cs * p.Hv + h) * D + row0;
+    const int clen = chunk_len(cs);
+#pragma unroll
+    for (int it = 0; it < NVIT; ++it) {
+      fv[it] = uint4{0u, 0u, 0u, 0u};
+      if (vrow[it] < clen) fv[it] = *reinterpret_cast<const uint4*>(vb + voff[it]);
+    }
+  };
+  auto diag_tile = [&](const ChunkBufs& cb, int lane) {
+    switch (si) {
+      case 0: diag_tile_of<0>(sm, cb, lane); break;
+      case 1: diag_tile_of<1>(sm, cb, lane); break;
+      case 2: diag_tile_of<2>(sm, cb, lane); break;
+      default: diag_tile_of<3>(sm, cb, lane); break;
+    }
+  };
+  auto ready = [&](int t, int lane) {
+    if (!V::kHooks || p.ready_chunks <= 0 || t < p.ready_chunks) signal_count(sm, kReady, lane);
+  };
+
+  ProducerPrefetch f = {};
+  uint4 fv[NVIT];
+  PhaseClock clk;
+  clk.start();
+  // Chunk 0 ahead of the loop: its gates, K/Q, and diagonal N tiles.
+  if (pw == 0) {
+    prefetch_gate_inputs(p, s0, chunk_len(s0), h, lane0, f);
+    store_gates(chunk_bufs(sm, 0), chunk_gates(f, lane0, chunk_len(s0), neg_decay, dt_bias), lane0);
+    signal_count(sm, kStaged, lane0);
+    if (nchunks > 1) prefetch_gate_inputs(p, s0 + C, chunk_len(s0 + C), h, lane0, f);
+  } else if (si >= 0) {
+    producer_prefetch(p, s0, chunk_len(s0), h, hq, hk, pt, lo, f);
+    load_v(fv, s0);
+    stage_kq(chunk_bufs(sm, 0), f, pt);
+    signal_count(sm, kStaged, lane0);
+    if (nchunks > 1) producer_prefetch(p, s0 + C, chunk_len(s0 + C), h, hq, hk, pt, lo, f);
+    wait_count<V::kHooks>(sm, kStaged, 5);
+    diag_tile(chunk_bufs(sm, 0), lane0);
+    signal_count(sm, kDiagN, lane0);
+  }
+  clk.lap(0);
+
+  for (int t = 0; t < nchunks; ++t) {
+    int lane = lane0;
+    asm volatile("" : "+v"(lane));
+    const int64_t cs = s0 + int64_t(t) * C;
+    const int64_t ncs = cs + C;
+    const ChunkBufs cb = chunk_bufs(sm, t & 1);
+    __builtin_amdgcn_s_setprio(1);
+    switch (pw) {
+      case 0:
+        wait_count<V::kHooks>(sm, kDiagN, 4 * (t + 1));
+        clk.lap(1);
+        diag_solve(sm, cb, lane);
+        signal_count(sm, kPPhase, lane);
+        clk.lap(2);
+        if (ncs < s1) {
+          // Chunk t + 1's gates, stored into the buffers of chunk t - 1 once consumed.
+          const ChunkGates g = chunk_gates(f, lane, chunk_len(ncs), neg_decay, dt_bias);
+          if (t >= 1) wait_count<V::kHooks>(sm, kConsumed, V::NCW * t);
+          clk.lap(3);
+          store_gates(chunk_bufs(sm, (t + 1) & 1), g, lane);
+          signal_count(sm, kStaged, lane);
+          if (ncs + C < s1) prefetch_gate_inputs(p, ncs + C, chunk_len(ncs + C), h, lane, f);
+        }
+        clk.lap(4);
+        break;
+      case 1: {
+        wait_count<V::kHooks>(sm, kStaged, 5 * (t + 1));
+        if (t >= 1) wait_count<V::kHooks>(sm, kNRead, t);  // chunk t - 1's N read by the left wave
+        clk.lap(1);
+        const TileJob j1[2] = {{1, 2, 1}, {1, 3, 2}};
+        run_tiles(sm, cb, j1, p.scale, lane);
+        const TileJob j2[2] = {{1, 3, 1}, {2, 3, 3}};
+        run_tiles(sm, cb, j2, p.scale, lane);
+        signal_count(sm, kPPhase, lane);
+        clk.lap(2);
+        wait_count<V::kHooks>(sm, kPPhase, 3 * (t + 1));
+        clk.lap(3);
+        offdiag_right(sm, cb, t, lane);
+        ready(t, lane);
+        clk.lap(4);
+        break;
+      }
+      case 3: {
+        wait_count<V::kHooks>(sm, kStaged, 5 * (t + 1));
+        clk.lap(1);
+        const TileJob j1[2] = {{1, 1, 0}, {1, 2, 0}};
+        run_tiles(sm, cb, j1, p.scale, lane);
+        const TileJob j2[2] = {{1, 3, 0}, {2, 2, 2}};
+        run_tiles(sm, cb, j2, p.scale, lane);
+        signal_count(sm, kPPhase, lane);
+        clk.lap(2);
+        wait_count<V::kHooks>(sm, kPPhase, 3 * (t + 1));
+        clk.lap(3);
+        offdiag_left<V::kHooks, true>(sm, cb, t, lane);
+        ready(t, lane);
+        clk.lap(4);
+        break;
+      }
+      default: {  // stagers
+        // Chunk t's V as soon as the consumers have read chunk t - 1's: with K, Q and
+        // the gates (staged a tick ahead) it is all their retrieve and Y need.
+        if (t >= 1) wait_count<V::kHooks>(sm, kVFree, V::NCW * t);
+#pragma unroll
+        for (int it = 0; it < NVIT; ++it) {
+          const int seg = pt + it * NPROD;
+          if (seg < V::VSEG)
+            *reinterpret_cast<uint4*>(sm.V + (seg / (V::ROWS / 8)) * VSTR + 8 * (seg % (V::ROWS / 8))) = fv[it];
+        }
+        signal_count(sm, kVStaged, lane);
+        if (ncs < s1) load_v(fv, ncs);  // chunk t + 1's V into registers
+        wait_count<V::kHooks>(sm, kStaged, 5 * (t + 1));  // chunk t's gates (wave 0)
+        clk.lap(1);
+        {
+          const TileJob jobs[4][2] = {{{2, 0, 0}, {2, 1, 0}}, {{2, 1, 1}, {2, 2, 0}}, {{2, 2, 1}, {2, 3, 0}},
+                                      {{2, 3, 1}, {2, 3, 2}}};
+          switch (si) {
+            case 0: run_tiles(sm, cb, jobs[0], p.scale, lane); break;
+            case 1: run_tiles(sm, cb, jobs[1], p.scale, lane); break;
+            case 2: run_tiles(sm, cb, jobs[2], p.scale, lane); break;
+            default: run_tiles(sm, cb, jobs[3], p.scale, lane); break;
+          }
+        }
+        ready(t, lane);  // chunk t's P tiles
+        clk.lap(2);
+        if (ncs < s1) {
+          // Chunk t + 1: K and Q into the buffers of chunk t - 1 once consumed; its
+          // diagonal N tiles once the solve of chunk t freed their scratch.
+          if (t >= 1) wait_count<V::kHooks>(sm, kConsumed, V::NCW * t);
+          clk.lap(3);
+          const ChunkBufs cbn = chunk_bufs(sm, (t + 1) & 1);
+          stage_kq(cbn, f, pt);
+          signal_count(sm, kStaged, lane);
+          if (ncs + C < s1) producer_prefetch(p, ncs + C, chunk_len(ncs + C), h, hq, hk, pt, lo, f);
+          wait_count<V::kHooks>(sm, kStaged, 5 * (t + 2));
+          wait_count<V::kHooks>(sm, kPPhase, 3 * (t + 1));
+          clk.lap(5);
+          diag_tile(cbn, lane);
+          signal_count(sm, kDiagN, lane);
+        }
+        clk.lap(4);
+        break;
+      }
+    }
+    __builtin_amdgcn_s_setprio(0);
   }
   clk.store(V::NCW + pw, lane0);
 }
@@ -1292,7 +1423,14 @@ __device__ __forceinline__ void consumer_loop(PrefillSmem& sm, const PrefillArgs
     const int64_t cs = s0 + int64_t(t - 1) * C;
     const int clen = int(s1 - cs < C ? s1 - cs : C);
     const ChunkBufs cb = chunk_bufs(sm, (t - 1) & 1);
-    wait_count<V::kHooks>(sm, kReady, 4 * t);  // chunk t - 1 prepared
+    if constexpr (V::NP == 7) {
+      // Seven producers hand a chunk over in two steps: K, Q, the gates and V for the
+      // retrieve and Y, then T~ and P ("ready", below) for v_new and the output.
+      wait_count<V::kHooks>(sm, kStaged, 5 * t);
+      wait_count<V::kHooks>(sm, kVStaged, 4 * t);
+    } else {
+      wait_count<V::kHooks>(sm, kReady, 4 * t);  // chunk t - 1 prepared
+    }
     clk.lap(0);
 
     // 1: X = K S^T, (Q S^T)^T
@@ -1322,6 +1460,7 @@ __device__ __forceinline__ void consumer_loop(PrefillSmem& sm, const PrefillArgs
       for (int vt = 0; vt < VT; ++vt) Xq[vt][ct] = Xq[vt][ct] * ecn;
     }
     signal_count(sm, kVFree, lane);  // V of this chunk read
+    if constexpr (V::NP == 7) wait_count<V::kHooks>(sm, kReady, 6 * t);  // T~ and P of this chunk
     clk.lap(2);
     // v_new = T~ Y (contraction over the rows of Y in blocks js; T~ is lower triangular).
     uint4 Yh[VT][2], Yl[VT][2];
@@ -1456,9 +1595,9 @@ __global__ __launch_bounds__(V::NTHREADS) void gdn_prefill_kernel(PrefillArgs p)
   // the natural order measured as fast or faster (two consumers on SIMDs of their
   // own: +1.5%; the producer variant's solve wave sharing a SIMD: +7%).
   // With seven producers (beside one consumer) the consumer keeps hardware wave 0 and
-  // shares its SIMD with the producer that has least to do (P tiles in step 2 only):
-  // hardware waves 1-7 take producers 0, 1, 3, 6, 4, 2, 5.
-  const int wave = V::NP == 7 ? (hw == 0 ? 0 : 1 + ((0x5246310 >> (4 * (hw - 1))) & 15))
+  // shares its SIMD with the producer that has least to do (wave 0, the solve): hardware
+  // waves 1-7 take producers 1, 2, 3, 0, 4, 5, 6.
+  const int wave = V::NP == 7 ? (hw == 0 ? 0 : 1 + ((0x6540321 >> (4 * (hw - 1))) & 15))
                    : !(V::kLoad && NCW == 1) ? hw
                    : hw == 3 ? 0 : hw < 3 ? hw + 1 : hw;
 
@@ -1498,7 +1637,7 @@ __global__ __launch_bounds__(V::NTHREADS) void gdn_prefill_kernel(PrefillArgs p)
         reinterpret_cast<uint4*>(sm.Nl)[e] = z;
       }
     }
-    if (tid < 8) sm.sync[tid] = 0;
+    if (tid < 16) sm.sync[tid] = 0;
     if (V::kHooks && tid == 0) {
       sm.spin_limit = p.spin_limit > 0 ? p.spin_limit : kSpinLimit;
       sm.aborts = p.aborts;
@@ -1513,7 +1652,11 @@ __global__ __launch_bounds__(V::NTHREADS) void gdn_prefill_kernel(PrefillArgs p)
         const u32x4* tiles = reinterpret_cast<const u32x4*>(p.tiles) + (int64_t(seq) * tc * p.Hv + h) * kTileImage;
         loader_loop<V>(sm, p, tiles, s0, s1, nchunks, h, hq, hk, row0, wave - NCW, lane0);
       } else {
-        producer_loop<V>(sm, p, s0, s1, nchunks, h, hq, hk, row0, wave - NCW, lane0);
+        if constexpr (V::NP == 7) {
+          producer_loop7<V>(sm, p, s0, s1, nchunks, h, hq, hk, row0, wave - NCW, lane0);
+        } else {
+          producer_loop<V>(sm, p, s0, s1, nchunks, h, hq, hk, row0, wave - NCW, lane0);
+        }
       }
     }
     return;
@@ -1616,7 +1759,7 @@ __global__ __launch_bounds__(PrepVariant::NTHREADS) void gdn_prefill_prep_kernel
       reinterpret_cast<uint4*>(sm.Nl)[e] = z;
     }
   }
-  if (tid < 8) sm.sync[tid] = 0;
+  if (tid < 16) sm.sync[tid] = 0;
   __syncthreads();
   u32x4* images = reinterpret_cast<u32x4*>(p.tiles) + ((int64_t(seq) * tc + t0) * p.Hv + h) * kTileImage;
   producer_loop<PrepVariant>(sm, p, cs, ce, nchunks, h, hq, hk, 0, wave, lane0, images);
