@@ -2,7 +2,8 @@
 //
 // A workgroup walks the chunks of one (sequence, v-head) chain, or of one slice
 // of its state rows, as a two-stage pipeline:
-//   * NP producer waves (NCW .. NCW+NP-1; four, or seven beside a single consumer)
+//   * NP producer waves (NCW .. NCW+NP-1; four, or seven beside one consumer and six
+//     beside two, which fill the workgroup's eight waves)
 //     prepare chunk t: stage K and Q in LDS, form the gates, the masked/decayed
 //     products N = strictLower(beta Gamma KK^T) and P = tril(Gamma QK^T), and
 //     T~ = (I + N)^-1;
@@ -20,8 +21,9 @@
 // each owning rows [R0, R0 + ROWS).  They all prepare the same chunk data (the
 // producer work does not depend on the state) and each stages only its slice of
 // V.  Batches with many chains use F = 1 (four consumer waves of 32 rows); few
-// chains are split so that every CU gets a workgroup (with F = 8 one 16-row
-// consumer and seven producers, whose repeated chunk preparation sets the pace).
+// chains are split so that every CU gets a workgroup (with F = 8 and F = 4 one or
+// two 16-row consumers beside seven or six pipelined producers, since the chunk
+// preparation, repeated in every slice, sets the pace).
 // When the caller provides
 // a workspace, batches split 4 or 8 ways run in two kernels instead: a prep kernel
 // prepares every chunk once (all chunks in parallel), and the state pass's loader
@@ -96,26 +98,32 @@ struct Variant {
   static constexpr int F = 128 / ROWS;           // workgroups per chain
   static constexpr int NTHREADS = 64 * (NCW + NP);
   static constexpr int VSEG = 8 * ROWS;          // 16-byte segments of the V slice of a chunk
+  // Seven producers beside one consumer, or six beside two, run pipelined one chunk
+  // deep (producer_loop_split) with NP - 3 stager waves, and hand a chunk to the
+  // consumers in two steps (K, Q, the gates and V; then T~ and P).
+  static constexpr bool kPipelined = NP_ >= 6;
+  static constexpr int kStagers = NP_ - 3;
   static_assert(F * ROWS == 128 && NCW + NP <= 8, "unsupported launch variant");
-  static_assert(NP == 4 || (NP == 7 && NCW == 1 && !LOAD_), "seven producers only beside one consumer");
+  static_assert(NP == 4 || (!LOAD_ && NCW + NP == 8 && NCW <= 2), "pipelined producers fill the workgroup");
 };
 
-// Production launch variants by split factor F (workgroups per chain).  With F = 8 a
-// chain's slice has one 16-row consumer wave and the chunk preparation, repeated in
-// every slice, sets the pace: seven producer waves share it.
+// Production launch variants by split factor F (workgroups per chain).  With F = 8
+// (F = 4) a chain's slice has one (two) 16-row consumer waves and the chunk
+// preparation, repeated in every slice, sets the pace: seven (six) pipelined
+// producer waves share it.
 template <bool HOOKS>
 using SplitVariant1 = Variant<4, 2, HOOKS>;
 template <bool HOOKS>
 using SplitVariant2 = Variant<4, 1, HOOKS>;
 template <bool HOOKS>
-using SplitVariant4 = Variant<2, 1, HOOKS>;
+using SplitVariant4 = Variant<2, 1, HOOKS, false, 6>;
 template <bool HOOKS>
 using SplitVariant8 = Variant<1, 1, HOOKS, false, 7>;
 
 // The prep kernel of the two-kernel path: the four producer waves alone (no
 // consumers, no V staging); they copy each chunk's tiles out themselves (kCopy).
 struct PrepVariant {
-  static constexpr bool kHooks = false, kLoad = false, kCopy = true;
+  static constexpr bool kHooks = false, kLoad = false, kCopy = true, kPipelined = false;
   static constexpr int NCW = 0, NP = 4, VT = 1, VW = 16, ROWS = 128, F = 1;
   static constexpr int NTHREADS = 64 * (NCW + 4);
   static constexpr int VSEG = 0;
@@ -789,33 +797,41 @@ __device__ __forceinline__ void offdiag_left(Smem& sm, const ChunkBufs& cb, int 
 // LDS reader) runs, so the stall overlaps LDS work that would hold them up
 // anyway.
 //
-// Producer thread pt (0..255) owns K/Q segments pt + 256 it (it = 0..3): token
-// pt/16 + 16 it, columns 8 (pt%16) .. +7 (16 consecutive threads read one
-// 256-byte row).  Addresses are a wave-uniform chunk base (64-bit, scalar) plus
-// a 32-bit lane offset that is fixed across chunks.
+// With NT threads sharing the K/Q rows of a chunk, thread pt (0..NT-1) owns K/Q
+// segments pt + NT it: token pt/16 + (NT/16) it, columns 8 (pt%16) .. +7 (16
+// consecutive threads read one 256-byte row); four producer waves (NT = 256) take
+// tokens pt/16 + 16 it, it = 0..3.  Addresses are a wave-uniform chunk base (64-bit,
+// scalar) plus a 32-bit lane offset that is fixed across chunks.
 constexpr int NPROD = 256;  // producer threads (four waves)
 
-struct ProducerPrefetch {
-  uint4 k[4], q[4];
-  uint16_t a, b;  // raw gate inputs of token pt (first producer wave only)
+template <int NT>
+struct ProducerPrefetchT {
+  static constexpr int RS = NT / 16;              // tokens between a thread's segments
+  static constexpr int NIT = (C + RS - 1) / RS;   // segments per thread
+  static_assert(NT % 64 == 0 && NT >= 64 && NT <= 256, "whole waves share the staging");
+  uint4 k[NIT], q[NIT];
+  uint16_t a, b;  // raw gate inputs of token pt (first wave only)
 };
+using ProducerPrefetch = ProducerPrefetchT<NPROD>;
 
 struct LaneOffsets {
   int k, q;  // (pt/16) rows + 8 (pt%16) elements, in the K and Q row strides
   int ab;    // pt rows of the a/b [T, Hv] layout
 };
 
+template <int NT>
 __device__ __forceinline__ void producer_prefetch(const PrefillArgs& p, int64_t cs, int clen, int h, int hq, int hk,
-                                                  int pt, const LaneOffsets& lo, ProducerPrefetch& f) {
+                                                  int pt, const LaneOffsets& lo, ProducerPrefetchT<NT>& f) {
+  constexpr int RS = ProducerPrefetchT<NT>::RS;
   const uint16_t* kb = p.k + (cs * p.Hk + hk) * D;
   const uint16_t* qb = p.q + (cs * p.Hq + hq) * D;
 #pragma unroll
-  for (int it = 0; it < 4; ++it) {
-    const int c = (pt >> 4) + 16 * it;
+  for (int it = 0; it < ProducerPrefetchT<NT>::NIT; ++it) {
+    const int c = (pt >> 4) + RS * it;
     f.k[it] = f.q[it] = uint4{0u, 0u, 0u, 0u};
     if (c < clen) {
-      f.k[it] = *reinterpret_cast<const uint4*>(kb + (lo.k + 16 * it * p.Hk * D));
-      f.q[it] = *reinterpret_cast<const uint4*>(qb + (lo.q + 16 * it * p.Hq * D));
+      f.k[it] = *reinterpret_cast<const uint4*>(kb + (lo.k + RS * it * p.Hk * D));
+      f.q[it] = *reinterpret_cast<const uint4*>(qb + (lo.q + RS * it * p.Hq * D));
     }
   }
   if (pt < 64) {  // wave-uniform; the row index is clamped and padding masked when used
@@ -832,7 +848,8 @@ struct ChunkGates {
   float gam, gaml, bet, eg, dd;
 };
 
-__device__ __forceinline__ ChunkGates chunk_gates(const ProducerPrefetch& f, int lane, int clen, float neg_decay,
+template <int NT>
+__device__ __forceinline__ ChunkGates chunk_gates(const ProducerPrefetchT<NT>& f, int lane, int clen, float neg_decay,
                                                   float dt_bias) {
   const float lg = lane < clen ? fast_log2_gate(neg_decay, bf16_to_f32(f.a) + dt_bias) : 0.f;
   ChunkGates g;
@@ -854,10 +871,13 @@ __device__ __forceinline__ void store_gates(const ChunkBufs& cb, const ChunkGate
 
 // Step 1 of a chunk: the prefetched K and Q rows into the chunk's tiles
 // (permuted columns).
-__device__ __forceinline__ void stage_kq(const ChunkBufs& cb, const ProducerPrefetch& f, int pt) {
+template <int NT>
+__device__ __forceinline__ void stage_kq(const ChunkBufs& cb, const ProducerPrefetchT<NT>& f, int pt) {
+  constexpr int RS = ProducerPrefetchT<NT>::RS;
 #pragma unroll
-  for (int it = 0; it < 4; ++it) {
-    const int c = (pt >> 4) + 16 * it, sg = pt & 15;
+  for (int it = 0; it < ProducerPrefetchT<NT>::NIT; ++it) {
+    const int c = (pt >> 4) + RS * it, sg = pt & 15;
+    if (RS * ProducerPrefetchT<NT>::NIT > C && c >= C) break;  // past the chunk (NT not dividing 1024)
     const int col0 = (8 * sg) & ~31, r0 = (8 * sg) & 31;
     const int pa = kq_off(c, col0 + perm32(r0)), pb = kq_off(c, col0 + perm32(r0 + 4));
     *reinterpret_cast<uint2*>(cb.K + pa) = uint2{f.k[it].x, f.k[it].y};
@@ -912,7 +932,7 @@ __device__ __forceinline__ void producer_loop(Smem& sm, const PrefillArgs& p, in
     vrow[it] = seg < V::VSEG ? c : C;  // C: no segment
     voff[it] = c * p.Hv * D + 8 * sg;
   }
-  static_assert(V::NP == 4, "seven producer waves run producer_loop7");
+  static_assert(V::NP == 4 && !V::kPipelined, "pipelined producers run producer_loop_split");
   ProducerPrefetch f;
   uint4 fv[NVIT];
   producer_prefetch(p, s0, int(s1 - s0 < C ? s1 - s0 : C), h, hq, hk, pt, lo, f);
@@ -1066,8 +1086,9 @@ __device__ __forceinline__ void producer_loop(Smem& sm, const PrefillArgs& p, in
 }
 
 // The raw gate inputs (a, b) of token `lane` of a chunk, clamped into the chunk.
+template <int NT>
 __device__ __forceinline__ void prefetch_gate_inputs(const PrefillArgs& p, int64_t cs, int clen, int h, int lane,
-                                                     ProducerPrefetch& f) {
+                                                     ProducerPrefetchT<NT>& f) {
   const int off = (lane < clen ? lane : clen - 1) * p.Hv;
   f.a = (p.a + cs * p.Hv + h)[off];
   f.b = (p.b + cs * p.Hv + h)[off];
@@ -1078,26 +1099,30 @@ __device__ __forceinline__ void diag_tile_of(Smem& sm, const ChunkBufs& cb, int 
   diag_tiles<SI, SI + 1>(sm, cb, lane);
 }
 
-// The producer loop with seven waves beside one consumer (chains split 8 ways),
-// pipelined one step deep.  For chunk t:
+// The producer loop of split chains, pipelined one step deep: seven producer
+// waves beside one consumer (chains split 8 ways) or six beside two (split 4
+// ways), with NS = NP - 3 of them stagers.  For chunk t:
 //   * wave 0 solves the diagonal blocks of T~ once chunk t's four diagonal N tiles
-//     are in, then forms chunk t + 1's gates;
+//     are in, then forms chunk t + 1's gates (and, with three stagers, chunk t + 1's
+//     last diagonal N tile);
 //   * waves 1 and 3 form the six off-diagonal N tiles (and one P tile each), then
 //     the off-diagonal blocks of T~ (offdiag_right, offdiag_left);
-//   * the stager waves 2, 4, 5 and 6 form the other eight P tiles and stage V, then
-//     stage chunk t + 1's K and Q and form its four diagonal N tiles,
+//   * the stager waves (2, 4, 5[, 6]) form the other eight P tiles and stage V, then
+//     stage chunk t + 1's K and Q and form its other diagonal N tiles,
 // so the solve of chunk t + 1 can start as soon as chunk t's is done, instead of
-// after chunk t + 1's staging and diagonal tiles.  Hand-offs per chunk: kStaged 5
-// (the stagers' K/Q and wave 0's gates), kDiagN 4, kPPhase 3 (the solve, and the N
-// tiles of waves 1 and 3), kNRead 1 (the left off-diagonal wave read its N operands,
-// so the next chunk's N tiles may overwrite them), kX32 1, kReady 6 (waves 1 and
-// 3, the stagers).  Every buffer of chunk t + 1's parity is written only after the
-// consumers signalled chunk t - 1 consumed.
+// after chunk t + 1's staging and diagonal tiles.  Hand-offs per chunk: kStaged
+// NS + 1 (the stagers' K/Q and wave 0's gates), kVStaged NS, kDiagN 4, kPPhase 3
+// (the solve, and the N tiles of waves 1 and 3), kNRead 1 (the left off-diagonal
+// wave read its N operands, so the next chunk's N tiles may overwrite them), kX32
+// 1, kReady NS + 2 (waves 1 and 3, the stagers).  Every buffer of chunk t + 1's
+// parity is written only after the consumers signalled chunk t - 1 consumed.
 template <class V>
-__device__ __forceinline__ void producer_loop7(PrefillSmem& sm, const PrefillArgs& p, int64_t s0, int64_t s1,
-                                               int nchunks, int h, int hq, int hk, int row0, int pw, int lane0) {
-  static_assert(V::NP == 7 && V::NCW == 1 && !V::kLoad && !V::kCopy, "seven-producer loop");
-  constexpr int NVIT = (V::VSEG + NPROD - 1) / NPROD;  // V segments per stager thread
+__device__ __forceinline__ void producer_loop_split(PrefillSmem& sm, const PrefillArgs& p, int64_t s0, int64_t s1,
+                                                    int nchunks, int h, int hq, int hk, int row0, int pw,
+                                                    int lane0) {
+  static_assert(V::kPipelined && !V::kLoad && !V::kCopy, "pipelined producer loop of split chains");
+  constexpr int NS = V::kStagers, NST = 64 * NS;        // stager waves, threads
+  constexpr int NVIT = (V::VSEG + NST - 1) / NST;       // V segments per stager thread
   const int si = pw == 2 ? 0 : pw >= 4 ? pw - 3 : -1;   // stager index (waves 2, 4, 5, 6)
   const int pt = (si < 0 ? 0 : si) * 64 + lane0;        // thread index among the stagers
   const float neg_decay = -expf(p.A_log[h]);
@@ -1106,7 +1131,7 @@ __device__ __forceinline__ void producer_loop7(PrefillSmem& sm, const PrefillArg
   int voff[NVIT], vrow[NVIT];
 #pragma unroll
   for (int it = 0; it < NVIT; ++it) {
-    const int seg = pt + it * NPROD, c = seg / (V::ROWS / 8), sg = seg % (V::ROWS / 8);
+    const int seg = pt + it * NST, c = seg / (V::ROWS / 8), sg = seg % (V::ROWS / 8);
     vrow[it] = seg < V::VSEG ? c : C;  // C: no segment
     voff[it] = c * p.Hv * D + 8 * sg;
   }
@@ -1120,6 +1145,7 @@ __device__ __forceinline__ void producer_loop7(PrefillSmem& sm, const PrefillArg
       if (vrow[it] < clen) fv[it] = *reinterpret_cast<const uint4*>(vb + voff[it]);
     }
   };
+  // Diagonal N tiles: stager si forms tile si; with three stagers wave 0 forms tile 3.
   auto diag_tile = [&](const ChunkBufs& cb, int lane) {
     switch (si) {
       case 0: diag_tile_of<0>(sm, cb, lane); break;
@@ -1131,8 +1157,31 @@ __device__ __forceinline__ void producer_loop7(PrefillSmem& sm, const PrefillArg
   auto ready = [&](int t, int lane) {
     if (!V::kHooks || p.ready_chunks <= 0 || t < p.ready_chunks) signal_count(sm, kReady, lane);
   };
+  // The stagers' eight P tiles (P(2,2) and P(3,3) go to waves 3 and 1).
+  auto stager_tiles = [&](const ChunkBufs& cb, int lane) {
+    if constexpr (NS == 4) {
+      const TileJob jobs[4][2] = {{{2, 0, 0}, {2, 1, 0}}, {{2, 1, 1}, {2, 2, 0}}, {{2, 2, 1}, {2, 3, 0}},
+                                  {{2, 3, 1}, {2, 3, 2}}};
+      switch (si) {
+        case 0: run_tiles(sm, cb, jobs[0], p.scale, lane); break;
+        case 1: run_tiles(sm, cb, jobs[1], p.scale, lane); break;
+        case 2: run_tiles(sm, cb, jobs[2], p.scale, lane); break;
+        default: run_tiles(sm, cb, jobs[3], p.scale, lane); break;
+      }
+    } else {
+      static_assert(NS == 3, "three or four stagers");
+      const TileJob a0[2] = {{2, 0, 0}, {2, 1, 0}}, a1[1] = {{2, 1, 1}};
+      const TileJob b0[2] = {{2, 2, 0}, {2, 2, 1}}, b1[1] = {{2, 3, 0}};
+      const TileJob c0[2] = {{2, 3, 1}, {2, 3, 2}};
+      switch (si) {
+        case 0: run_tiles(sm, cb, a0, p.scale, lane); run_tiles(sm, cb, a1, p.scale, lane); break;
+        case 1: run_tiles(sm, cb, b0, p.scale, lane); run_tiles(sm, cb, b1, p.scale, lane); break;
+        default: run_tiles(sm, cb, c0, p.scale, lane); break;
+      }
+    }
+  };
 
-  ProducerPrefetch f = {};
+  ProducerPrefetchT<NST> f = {};
   uint4 fv[NVIT];
   PhaseClock clk;
   clk.start();
@@ -1142,13 +1191,18 @@ __device__ __forceinline__ void producer_loop7(PrefillSmem& sm, const PrefillArg
     store_gates(chunk_bufs(sm, 0), chunk_gates(f, lane0, chunk_len(s0), neg_decay, dt_bias), lane0);
     signal_count(sm, kStaged, lane0);
     if (nchunks > 1) prefetch_gate_inputs(p, s0 + C, chunk_len(s0 + C), h, lane0, f);
+    if constexpr (NS == 3) {
+      wait_count<V::kHooks>(sm, kStaged, NS + 1);
+      diag_tile_of<3>(sm, chunk_bufs(sm, 0), lane0);
+      signal_count(sm, kDiagN, lane0);
+    }
   } else if (si >= 0) {
     producer_prefetch(p, s0, chunk_len(s0), h, hq, hk, pt, lo, f);
     load_v(fv, s0);
     stage_kq(chunk_bufs(sm, 0), f, pt);
     signal_count(sm, kStaged, lane0);
     if (nchunks > 1) producer_prefetch(p, s0 + C, chunk_len(s0 + C), h, hq, hk, pt, lo, f);
-    wait_count<V::kHooks>(sm, kStaged, 5);
+    wait_count<V::kHooks>(sm, kStaged, NS + 1);
     diag_tile(chunk_bufs(sm, 0), lane0);
     signal_count(sm, kDiagN, lane0);
   }
@@ -1173,14 +1227,22 @@ __device__ __forceinline__ void producer_loop7(PrefillSmem& sm, const PrefillArg
           const ChunkGates g = chunk_gates(f, lane, chunk_len(ncs), neg_decay, dt_bias);
           if (t >= 1) wait_count<V::kHooks>(sm, kConsumed, V::NCW * t);
           clk.lap(3);
-          store_gates(chunk_bufs(sm, (t + 1) & 1), g, lane);
+          const ChunkBufs cbn = chunk_bufs(sm, (t + 1) & 1);
+          store_gates(cbn, g, lane);
           signal_count(sm, kStaged, lane);
           if (ncs + C < s1) prefetch_gate_inputs(p, ncs + C, chunk_len(ncs + C), h, lane, f);
+          if constexpr (NS == 3) {
+            // Chunk t + 1's last diagonal N tile, once its K is staged (the solve of
+            // chunk t, just done, freed the scratch).
+            wait_count<V::kHooks>(sm, kStaged, (NS + 1) * (t + 2));
+            diag_tile_of<3>(sm, cbn, lane);
+            signal_count(sm, kDiagN, lane);
+          }
         }
         clk.lap(4);
         break;
       case 1: {
-        wait_count<V::kHooks>(sm, kStaged, 5 * (t + 1));
+        wait_count<V::kHooks>(sm, kStaged, (NS + 1) * (t + 1));
         if (t >= 1) wait_count<V::kHooks>(sm, kNRead, t);  // chunk t - 1's N read by the left wave
         clk.lap(1);
         const TileJob j1[2] = {{1, 2, 1}, {1, 3, 2}};
@@ -1197,7 +1259,7 @@ __device__ __forceinline__ void producer_loop7(PrefillSmem& sm, const PrefillArg
         break;
       }
       case 3: {
-        wait_count<V::kHooks>(sm, kStaged, 5 * (t + 1));
+        wait_count<V::kHooks>(sm, kStaged, (NS + 1) * (t + 1));
         clk.lap(1);
         const TileJob j1[2] = {{1, 1, 0}, {1, 2, 0}};
         run_tiles(sm, cb, j1, p.scale, lane);
@@ -1218,24 +1280,15 @@ __device__ __forceinline__ void producer_loop7(PrefillSmem& sm, const PrefillArg
         if (t >= 1) wait_count<V::kHooks>(sm, kVFree, V::NCW * t);
 #pragma unroll
         for (int it = 0; it < NVIT; ++it) {
-          const int seg = pt + it * NPROD;
+          const int seg = pt + it * NST;
           if (seg < V::VSEG)
             *reinterpret_cast<uint4*>(sm.V + (seg / (V::ROWS / 8)) * VSTR + 8 * (seg % (V::ROWS / 8))) = fv[it];
         }
         signal_count(sm, kVStaged, lane);
         if (ncs < s1) load_v(fv, ncs);  // chunk t + 1's V into registers
-        wait_count<V::kHooks>(sm, kStaged, 5 * (t + 1));  // chunk t's gates (wave 0)
+        wait_count<V::kHooks>(sm, kStaged, (NS + 1) * (t + 1));  // chunk t's gates (wave 0)
         clk.lap(1);
-        {
-          const TileJob jobs[4][2] = {{{2, 0, 0}, {2, 1, 0}}, {{2, 1, 1}, {2, 2, 0}}, {{2, 2, 1}, {2, 3, 0}},
-                                      {{2, 3, 1}, {2, 3, 2}}};
-          switch (si) {
-            case 0: run_tiles(sm, cb, jobs[0], p.scale, lane); break;
-            case 1: run_tiles(sm, cb, jobs[1], p.scale, lane); break;
-            case 2: run_tiles(sm, cb, jobs[2], p.scale, lane); break;
-            default: run_tiles(sm, cb, jobs[3], p.scale, lane); break;
-          }
-        }
+        stager_tiles(cb, lane);
         ready(t, lane);  // chunk t's P tiles
         clk.lap(2);
         if (ncs < s1) {
@@ -1247,7 +1300,7 @@ __device__ __forceinline__ void producer_loop7(PrefillSmem& sm, const PrefillArg
           stage_kq(cbn, f, pt);
           signal_count(sm, kStaged, lane);
           if (ncs + C < s1) producer_prefetch(p, ncs + C, chunk_len(ncs + C), h, hq, hk, pt, lo, f);
-          wait_count<V::kHooks>(sm, kStaged, 5 * (t + 2));
+          wait_count<V::kHooks>(sm, kStaged, (NS + 1) * (t + 2));
           wait_count<V::kHooks>(sm, kPPhase, 3 * (t + 1));
           clk.lap(5);
           diag_tile(cbn, lane);
@@ -1423,11 +1476,11 @@ __device__ __forceinline__ void consumer_loop(PrefillSmem& sm, const PrefillArgs
     const int64_t cs = s0 + int64_t(t - 1) * C;
     const int clen = int(s1 - cs < C ? s1 - cs : C);
     const ChunkBufs cb = chunk_bufs(sm, (t - 1) & 1);
-    if constexpr (V::NP == 7) {
-      // Seven producers hand a chunk over in two steps: K, Q, the gates and V for the
-      // retrieve and Y, then T~ and P ("ready", below) for v_new and the output.
-      wait_count<V::kHooks>(sm, kStaged, 5 * t);
-      wait_count<V::kHooks>(sm, kVStaged, 4 * t);
+    if constexpr (V::kPipelined) {
+      // Pipelined producers hand a chunk over in two steps: K, Q, the gates and V for
+      // the retrieve and Y, then T~ and P ("ready", below) for v_new and the output.
+      wait_count<V::kHooks>(sm, kStaged, (V::kStagers + 1) * t);
+      wait_count<V::kHooks>(sm, kVStaged, V::kStagers * t);
     } else {
       wait_count<V::kHooks>(sm, kReady, 4 * t);  // chunk t - 1 prepared
     }
@@ -1460,7 +1513,7 @@ __device__ __forceinline__ void consumer_loop(PrefillSmem& sm, const PrefillArgs
       for (int vt = 0; vt < VT; ++vt) Xq[vt][ct] = Xq[vt][ct] * ecn;
     }
     signal_count(sm, kVFree, lane);  // V of this chunk read
-    if constexpr (V::NP == 7) wait_count<V::kHooks>(sm, kReady, 6 * t);  // T~ and P of this chunk
+    if constexpr (V::kPipelined) wait_count<V::kHooks>(sm, kReady, (V::kStagers + 2) * t);  // T~ and P
     clk.lap(2);
     // v_new = T~ Y (contraction over the rows of Y in blocks js; T~ is lower triangular).
     uint4 Yh[VT][2], Yl[VT][2];
@@ -1596,8 +1649,13 @@ __global__ __launch_bounds__(V::NTHREADS) void gdn_prefill_kernel(PrefillArgs p)
   // own: +1.5%; the producer variant's solve wave sharing a SIMD: +7%).
   // With seven producers (beside one consumer) the consumer keeps hardware wave 0 and
   // shares its SIMD with the producer that has least to do (wave 0, the solve): hardware
-  // waves 1-7 take producers 1, 2, 3, 0, 4, 5, 6.
-  const int wave = V::NP == 7 ? (hw == 0 ? 0 : 1 + ((0x6540321 >> (4 * (hw - 1))) & 15))
+  // waves 1-7 take producers 1, 2, 3, 0, 4, 5, 6.  With six (beside two consumers on
+  // hardware waves 0 and 1) hardware waves 2-7 take producers 2, 3, 0, 5, 1, 4: the
+  // consumers share their SIMDs with the solve wave and the third stager, and each
+  // off-diagonal wave shares one with a stager (1.5-2.5% faster than pairing the
+  // second consumer with the right off-diagonal wave, or the two off-diagonal waves).
+  const int wave = V::NP == 7   ? (hw == 0 ? 0 : 1 + ((0x6540321 >> (4 * (hw - 1))) & 15))
+                   : V::NP == 6 ? (hw < 2 ? hw : 2 + ((0x415032 >> (4 * (hw - 2))) & 15))
                    : !(V::kLoad && NCW == 1) ? hw
                    : hw == 3 ? 0 : hw < 3 ? hw + 1 : hw;
 
@@ -1652,8 +1710,8 @@ __global__ __launch_bounds__(V::NTHREADS) void gdn_prefill_kernel(PrefillArgs p)
         const u32x4* tiles = reinterpret_cast<const u32x4*>(p.tiles) + (int64_t(seq) * tc * p.Hv + h) * kTileImage;
         loader_loop<V>(sm, p, tiles, s0, s1, nchunks, h, hq, hk, row0, wave - NCW, lane0);
       } else {
-        if constexpr (V::NP == 7) {
-          producer_loop7<V>(sm, p, s0, s1, nchunks, h, hq, hk, row0, wave - NCW, lane0);
+        if constexpr (V::kPipelined) {
+          producer_loop_split<V>(sm, p, s0, s1, nchunks, h, hq, hk, row0, wave - NCW, lane0);
         } else {
           producer_loop<V>(sm, p, s0, s1, nchunks, h, hq, hk, row0, wave - NCW, lane0);
         }

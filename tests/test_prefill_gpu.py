@@ -393,7 +393,7 @@ def test_prefill_workspace_reuse(gpu):
 
 
 @pytest.mark.giveups_expected
-@pytest.mark.parametrize("heads,split", [(Heads(16, 16, 32), 2), (Heads(4, 4, 8), 8)])
+@pytest.mark.parametrize("heads,split", [(Heads(16, 16, 32), 2), (Heads(8, 8, 16), 4), (Heads(4, 4, 8), 8)])
 def test_prefill_bounded_waits(gpu, heads, split):
     """The hand-off failure path, forced from the host.  With the testing hooks off
     the entry point is gdn_prefill bit for bit and nothing gives up.  With the
@@ -404,7 +404,8 @@ def test_prefill_bounded_waits(gpu, heads, split):
     gdn_prefill_giveups reports, every output and final-state element of the affected
     sequences is NaN, the one-chunk sequence's results are untouched, and the next
     normal launch is exact again.  With 32 v-heads the 96 chains split 2 ways (four
-    producer waves per workgroup); with 8 the 24 chains split 8 ways (seven)."""
+    producer waves per workgroup); with 16 the 48 chains split 4 ways (six, pipelined);
+    with 8 the 24 chains split 8 ways (seven, pipelined)."""
     lens = [300, 130, 40]             # 5, 3 and 1 chunks
     p = workloads.prefill_inputs(lens, heads, seed=21, gate="slow", state_scale=0.5)
     binding.prefill_giveups(reset=True)
