@@ -1424,6 +1424,37 @@ __device__ __forceinline__ void retrieve(const ChunkBufs& cb, const f32x4 (&S)[V
   for (int ct = 0; ct < 4; ++ct)
 #pragma unroll
     for (int vt = 0; vt < VT; ++vt) Xk[ct][vt] = Xq[vt][ct] = zero4();
+  if constexpr (VT == 1) {
+    // One state tile leaves registers for the next contraction block's K and Q
+    // fragments: they are read while this block's MFMAs run (the scheduling
+    // barrier keeps the reads ahead of them).
+    uint4 kf[2][4], qf[2][4];
+#pragma unroll
+    for (int ct = 0; ct < 4; ++ct) {
+      kf[0][ct] = frag_kq(cb.K, 16 * ct, 0, lane);
+      qf[0][ct] = frag_kq(cb.Q, 16 * ct, 0, lane);
+    }
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      if (ks < 3) {
+#pragma unroll
+        for (int ct = 0; ct < 4; ++ct) {
+          kf[(ks + 1) & 1][ct] = frag_kq(cb.K, 16 * ct, ks + 1, lane);
+          qf[(ks + 1) & 1][ct] = frag_kq(cb.Q, 16 * ct, ks + 1, lane);
+        }
+      }
+      __builtin_amdgcn_sched_barrier(0);
+      uint4 Sh, Sl;
+      split_pack(S[0][2 * ks], S[0][2 * ks + 1], Sh, Sl);
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct) {
+        Xk[ct][0] = mfma(kf[ks & 1][ct], Sh, Xk[ct][0]);
+        Xk[ct][0] = mfma(kf[ks & 1][ct], Sl, Xk[ct][0]);
+        Xq[0][ct] = mfma(Sh, qf[ks & 1][ct], Xq[0][ct]);
+      }
+    }
+    return;
+  }
 #pragma unroll
   for (int ks = 0; ks < 4; ++ks) {
     uint4 Sh[VT], Sl[VT];
