@@ -1546,6 +1546,27 @@ __device__ __forceinline__ void consumer_loop(PrefillSmem& sm, const PrefillArgs
     signal_count(sm, kVFree, lane);  // V of this chunk read
     if constexpr (V::kPipelined) wait_count<V::kHooks>(sm, kReady, (V::kStagers + 2) * t);  // T~ and P
     clk.lap(2);
+    // The 16-row consumer reads all its T~ and P operands now (they are ready), so that
+    // their latency overlaps the Y split; the 32-row one, short of registers, as used.
+    // Pair (ct, js) of T~ is fragment ct < 2 ? ct : 2 ct - 2 + js; pair (js, ct) of
+    // P is fragment js ? ct + 2 : ct.
+    constexpr int NPF = VT == 1 ? 6 : 1;
+    uint4 thf[NPF], tlf[NPF], pqf[NPF];
+    if constexpr (VT == 1) {
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct)
+#pragma unroll
+        for (int js = 0; js <= (ct >> 1); ++js) {
+          const int i = ct < 2 ? ct : 2 * ct - 2 + js;
+          thf[i] = frag(cb.Th, TSTR, 16 * ct, js, lane);
+          tlf[i] = frag(cb.Tl, TSTR, 16 * ct, js, lane);
+        }
+#pragma unroll
+      for (int js = 0; js < 2; ++js)
+#pragma unroll
+        for (int ct = 2 * js; ct < 4; ++ct) pqf[js ? ct + 2 : ct] = frag(cb.P, TSTR, 16 * ct, js, lane);
+      __builtin_amdgcn_sched_barrier(0);
+    }
     // v_new = T~ Y (contraction over the rows of Y in blocks js; T~ is lower triangular).
     uint4 Yh[VT][2], Yl[VT][2];
 #pragma unroll
@@ -1559,8 +1580,14 @@ __device__ __forceinline__ void consumer_loop(PrefillSmem& sm, const PrefillArgs
       for (int vt = 0; vt < VT; ++vt) Vn[ct][vt] = zero4();
 #pragma unroll
       for (int js = 0; js <= (ct >> 1); ++js) {
-        const uint4 th = frag(cb.Th, TSTR, 16 * ct, js, lane);
-        const uint4 tl = frag(cb.Tl, TSTR, 16 * ct, js, lane);
+        uint4 th, tl;
+        if constexpr (VT == 1) {
+          th = thf[ct < 2 ? ct : 2 * ct - 2 + js];
+          tl = tlf[ct < 2 ? ct : 2 * ct - 2 + js];
+        } else {
+          th = frag(cb.Th, TSTR, 16 * ct, js, lane);
+          tl = frag(cb.Tl, TSTR, 16 * ct, js, lane);
+        }
 #pragma unroll
         for (int vt = 0; vt < VT; ++vt) {
           Vn[ct][vt] = mfma(th, Yh[vt][js], Vn[ct][vt]);
@@ -1578,7 +1605,12 @@ __device__ __forceinline__ void consumer_loop(PrefillSmem& sm, const PrefillArgs
       for (int vt = 0; vt < VT; ++vt) vb[vt] = pack_hi(Vn[2 * js][vt], Vn[2 * js + 1][vt]);
 #pragma unroll
       for (int ct = 2 * js; ct < 4; ++ct) {
-        const uint4 pq = frag(cb.P, TSTR, 16 * ct, js, lane);
+        uint4 pq;
+        if constexpr (VT == 1) {
+          pq = pqf[js ? ct + 2 : ct];
+        } else {
+          pq = frag(cb.P, TSTR, 16 * ct, js, lane);
+        }
 #pragma unroll
         for (int vt = 0; vt < VT; ++vt) Xq[vt][ct] = mfma(vb[vt], pq, Xq[vt][ct]);
       }
