@@ -404,16 +404,16 @@ namespace {
 // signals by adding 1 after all its earlier LDS accesses completed (release); a
 // waiter polls until the count reaches its target (acquire).
 enum SyncCounter {
-  kReady = 0,     // chunk handed over to the consumers (4 a chunk; seven producers: its T~ and P, 6)
+  kReady = 0,     // chunk handed over to the consumers (4 a chunk; pipelined: its T~ and P, NS + 2)
   kVFree = 1,     // consumers read the chunk's V
   kConsumed = 2,  // consumers done with the chunk's buffers
-  kPPhase = 3,    // four producers: their step barriers; seven: solve and N tiles done (3 a chunk)
+  kPPhase = 3,    // four producers: their step barriers; pipelined: solve and N tiles done (3 a chunk)
   kAbort = 4,     // a wait gave up
   kDiagN = 5,     // diagonal N tiles formed (4 a chunk)
   kX32 = 6,       // off-diagonal block X32 stored
-  kStaged = 7,    // seven producers: the chunk's K/Q staged and its gates stored (5 a chunk)
-  kNRead = 8,     // seven producers: the left off-diagonal wave read its N operands
-  kVStaged = 9    // seven producers: the chunk's V staged (4 a chunk)
+  kStaged = 7,    // pipelined: the chunk's K/Q staged and its gates stored (NS + 1 a chunk)
+  kNRead = 8,     // pipelined: the left off-diagonal wave read its N operands
+  kVStaged = 9    // pipelined: the chunk's V staged (NS a chunk)
 };
 constexpr int kSpinLimit = 1 << 21;  // default polls (about 70 ms) before a wait gives up
 
