@@ -1531,7 +1531,6 @@ __device__ __forceinline__ void consumer_loop(PrefillSmem& sm, const PrefillArgs
       const float b4[4] = {bc.x, bc.y, bc.z, bc.w}, e4[4] = {ec.x, ec.y, ec.z, ec.w};
 #pragma unroll
       for (int vt = 0; vt < VT; ++vt) {
-        // V rows 16ct + 4g .. +3 of column VW w + 16vt + n16 (zero past the chunk end)
         // V rows 16ct + 4g .. +3 of column VW w + vrow(vt, n16): lane j of a 16-lane
         // group reads the 4 columns VW w + vrow(vt, 4 (j & 3)) .. +3 of row 16ct + 4g + j/4.
         const uint2 vv = read_tr(sm.V + (16 * ct + 4 * g + (n16 >> 2)) * VSTR + VW * wave + vrow<VT>(vt, 4 * (n16 & 3)));
