@@ -51,7 +51,7 @@ def test_prefill_null_state_and_cu_dtypes(gpu, cu_dtype):
     assert not host(ns)[2].any()                      # empty sequence, zero initial state
 
 
-@pytest.mark.parametrize("lens", [[100, 0, 20], [100, 20]])   # 96 chains: one kernel; 64: two
+@pytest.mark.parametrize("lens", [[100, 0, 20], [100, 20]])   # 96 chains split 2 ways; 64 split 4 ways
 def test_prefill_in_place(gpu, lens):
     say(f"prefill in place lens={lens}")
     p = workloads.prefill_inputs(lens, seed=12, gate="slow", state_scale=0.5)
