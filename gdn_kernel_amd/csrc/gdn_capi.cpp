@@ -33,6 +33,8 @@ constexpr int64_t kMaxGrid = 0x7fffffff;
 // A launch's grid times its workgroup size (work-items per dimension) must fit in
 // 32 bits.
 constexpr int64_t kMaxWorkItems = 0xffffffffLL;
+static_assert(int64_t(64 + 16) * GDN_MAX_HEADS * 128 < (int64_t(1) << 31),
+              "per-chunk row offsets of GDN_MAX_HEADS heads fit 32 bits");
 static_assert(GDN_PREFILL_NO_ALLOC_SCRATCH_BYTES == gdn::kPrefillScratchBytes,
               "the header's scratch size must match the library's");
 
@@ -42,6 +44,11 @@ int check_heads(int32_t hq, int32_t hk, int32_t hv, int32_t dk, int32_t dv) {
   if (hv % hq != 0 || hv % hk != 0)
     return fail(GDN_ERR_INVALID_ARGUMENT,
                 "num_v_heads (%d) must be a multiple of num_q_heads (%d) and num_k_heads (%d)", hv, hq, hk);
+  // Per-chunk row offsets in the kernels (up to 64 tokens x heads x 128 elements) are
+  // 32-bit; num_q_heads and num_k_heads divide num_v_heads, so bounding it bounds all.
+  if (hv > GDN_MAX_HEADS)
+    return fail(GDN_ERR_UNSUPPORTED, "num_v_heads (%d) is above the %d heads the kernels address", hv,
+                GDN_MAX_HEADS);
   if (dk <= 0 || dv <= 0)
     return fail(GDN_ERR_INVALID_ARGUMENT, "head dims must be positive (dk=%d dv=%d)", dk, dv);
   if (dk != kD || dv != kD)

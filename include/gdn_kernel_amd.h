@@ -37,6 +37,11 @@ typedef uint16_t gdn_bf16; /* raw bf16 bits */
 #define GDN_INDEX_INT32 0
 #define GDN_INDEX_INT64 1
 
+/* Largest head count (num_q_heads, num_k_heads, num_v_heads) the kernels address:
+ * their per-chunk row offsets (up to 64 tokens x heads x 128 elements) are 32-bit.
+ * Larger counts return GDN_ERR_UNSUPPORTED. */
+#define GDN_MAX_HEADS 65536
+
 /* Library version, as MAJOR*10000 + MINOR*100 + PATCH. */
 int gdn_version(void);
 

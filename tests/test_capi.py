@@ -110,6 +110,20 @@ def pre_args(**kw):
                            "dk", "dv")]
 
 
+def test_head_count_limit(lib):
+    """Head counts up to GDN_MAX_HEADS (65,536) pass validation; above it both entry
+    points refuse with GDN_ERR_UNSUPPORTED before any device call (the kernels' per-chunk
+    row offsets are 32-bit)."""
+    limit = 65536
+    far = FAKE + (1 << 44)   # new_state well clear of the (huge) state range
+    assert lib.gdn_prefill_check(*pre_args(N=1, T=64, Hq=1, Hk=1, Hv=limit, new_state=far)) == OK
+    assert lib.gdn_decode_check(*dec_args(B=1, Hq=1, Hk=1, Hv=limit, new_state=far)) == OK
+    assert lib.gdn_prefill_check(*pre_args(N=1, T=64, Hq=1, Hk=1, Hv=2 * limit, new_state=far)) == UNSUPPORTED
+    assert "num_v_heads" in _lib.last_error()
+    assert lib.gdn_decode_check(*dec_args(B=1, Hq=1, Hk=1, Hv=2 * limit, new_state=far)) == UNSUPPORTED
+    assert "num_v_heads" in _lib.last_error()
+
+
 def test_prefill_check_accepts_valid(lib):
     assert lib.gdn_prefill_check(*pre_args()) == OK
     assert lib.gdn_prefill_check(*pre_args(cu_dtype=_lib.GDN_INDEX_INT64)) == OK
