@@ -1,6 +1,7 @@
 """CPU tests of the C ABI: the library loads, exports every symbol the header
 declares, and validates arguments before any device call (these run without a
 GPU; no compute entry point is called with valid arguments here)."""
+import os
 import ctypes
 import re
 import subprocess
@@ -108,6 +109,20 @@ def pre_args(**kw):
     return [a[k] for k in ("q", "k", "v", "state", "A_log", "a", "dt_bias", "b", "cu",
                            "cu_dtype", "N", "T", "scale", "output", "new_state", "Hq", "Hk", "Hv",
                            "dk", "dv")]
+
+
+def test_header_constants_match_the_python_binding():
+    """Every integer #define of include/gdn_kernel_amd.h (a literal, or a literal shifted
+    left) has the same value in _lib."""
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    text = open(os.path.join(root, "include", "gdn_kernel_amd.h")).read()
+    defs = dict(re.findall(r"^#define (GDN_[A-Z0-9_]+) \(?([0-9LL <]+?)\)?\s*(?:/\*.*)?$", text, re.M))
+    assert {"GDN_OK", "GDN_ERR_UNSUPPORTED", "GDN_INDEX_INT64", "GDN_MAX_HEADS",
+            "GDN_PREFILL_NO_ALLOC_SCRATCH_BYTES"} <= set(defs)
+    for name, value in defs.items():
+        parts = [int(x.strip().rstrip("L")) for x in value.split("<<")]
+        expected = parts[0] << parts[1] if len(parts) == 2 else parts[0]
+        assert getattr(_lib, name) == expected, name
 
 
 def test_head_count_limit(lib):
