@@ -14,7 +14,7 @@ from tests.gpu_util import say
 
 pytestmark = pytest.mark.gpu
 
-SCRATCH_BYTES = 64 << 20
+SCRATCH_BYTES = _lib.GDN_PREFILL_NO_ALLOC_SCRATCH_BYTES  # 64 MiB, as in the header
 
 
 def _call(lib, fn, p, gpu, ws=None):
