@@ -213,3 +213,22 @@ def test_decode_every_launch_shape(gpu):
         torch.cuda.synchronize()
         assert_close(host(out), op_ref, OUT_RTOL, OUT_ATOL, f"shape {variant} pooled output")
         assert_close(host(pool), pool_ref, STATE_RTOL, STATE_ATOL, f"shape {variant} pool")
+
+
+def test_decode_max_heads(gpu):
+    """The largest head count the C ABI accepts (GDN_MAX_HEADS = 65,536 q, k and v heads),
+    B = 2, state updated in place: every output element is written, and five heads at
+    both ends and in the middle match the oracle run on those heads alone."""
+    h = _lib.GDN_MAX_HEADS
+    say(f"decode max heads Hq=Hk=Hv={h} B=2")
+    w = workloads.decode_inputs(2, Heads(h, h, h), seed=78, device=gpu, gate="slow", state_scale=0.5)
+    gi = torch.tensor([0, 1, h // 2 + 3, h - 2, h - 1], device=gpu)
+    sub = {k: w[k][:, :, gi].cpu() for k in ("q", "k", "v", "a", "b")}
+    sub.update({k: w[k][gi].cpu() for k in ("A_log", "dt_bias")})
+    sub["state"], sub["scale"] = w["state"][:, gi].cpu(), w["scale"]
+    out, ns = run_decode(w, gpu, in_place=True)
+    torch.cuda.synchronize()
+    assert not torch.isnan(out).any()
+    o_ref, s_ref = oracle_decode(sub)
+    assert_close(host(out[:, :, gi]), o_ref, OUT_RTOL, OUT_ATOL, "output")
+    assert_close(host(ns[:, gi]), s_ref, STATE_RTOL, STATE_ATOL, "new_state")

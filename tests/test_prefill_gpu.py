@@ -457,3 +457,32 @@ def test_prefill_random_batches(gpu, seed):
     torch.cuda.synchronize()
     assert_close(host(out), o_ref, OUT_RTOL, OUT_ATOL, "output")
     assert_close(host(ns), s_ref, STATE_RTOL, STATE_ATOL, "new_state")
+
+
+def _heads_of(p, idx):
+    """The inputs of v-heads ``idx`` alone, on the CPU (q/k heads likewise: the test's
+    head counts are equal)."""
+    gi = idx.to(p["q"].device)
+    sub = {k: p[k][:, gi].cpu() for k in ("q", "k", "v", "a", "b")}
+    sub.update({k: p[k][gi].cpu() for k in ("A_log", "dt_bias")})
+    sub["state"] = None if p["state"] is None else p["state"][:, gi].cpu()
+    sub["cu_seqlens"], sub["scale"] = p["cu_seqlens"].cpu(), p["scale"]
+    return sub
+
+
+def test_prefill_max_heads(gpu):
+    """The largest head count the C ABI accepts (GDN_MAX_HEADS = 65,536 q, k and v heads),
+    one 80-token sequence (a full chunk and a partial one): per-chunk row offsets are
+    at their largest.  Every output element is written, and five heads at both ends and
+    in the middle match the oracle run on those heads alone."""
+    h = _lib.GDN_MAX_HEADS
+    say(f"prefill max heads Hq=Hk=Hv={h} lens=[80]")
+    p = workloads.prefill_inputs([80], Heads(h, h, h), seed=77, device=gpu, gate="slow",
+                                 state_scale=0.5)
+    out, ns = run_prefill(p, gpu)
+    torch.cuda.synchronize()
+    assert not torch.isnan(out).any() and not torch.isnan(ns).any()
+    idx = torch.tensor([0, 1, h // 2 + 3, h - 2, h - 1])
+    o_ref, s_ref = oracle_prefill(_heads_of(p, idx))
+    assert_close(host(out[:, idx.to(gpu)]), o_ref, OUT_RTOL, OUT_ATOL, "output")
+    assert_close(host(ns[:, idx.to(gpu)]), s_ref, STATE_RTOL, STATE_ATOL, "new_state")
