@@ -91,7 +91,7 @@ struct Variant {
   static constexpr bool kLoad = LOAD_;           // waves NCW.. load prepared T~/P (two-kernel path)
   static constexpr bool kCopy = false;           // producers copy their tiles out (prep kernel only)
   static constexpr int NCW = NCW_;               // consumer waves
-  static constexpr int NP = NP_;                 // producer (or loader) waves: 4, or 7 beside one consumer
+  static constexpr int NP = NP_;                 // producer (or loader) waves: 4; or 7 (6) beside one (two) consumers
   static constexpr int VT = VT_;                 // 16-row state tiles per consumer wave
   static constexpr int VW = 16 * VT;             // state rows per consumer wave
   static constexpr int ROWS = NCW * VW;          // state rows per workgroup
