@@ -85,7 +85,7 @@ constexpr int TSTR = 72;     // bf16 row stride of 64-wide tiles (T~, P, N)
 constexpr int NDB = 16 * 16 + 4;  // floats per diagonal N block (column-major; padded by 16 bytes)
 constexpr int NROWS = C - 16;  // rows of N kept for the off-diagonal solve
 
-template <int NCW_, int VT_, bool HOOKS_ = false, bool LOAD_ = false, int NP_ = 4>
+template <int NCW_, int VT_, bool HOOKS_ = false, bool LOAD_ = false, int NP_ = 4, bool PERSIST_ = false>
 struct Variant {
   static constexpr bool kHooks = HOOKS_;         // testing hooks of PrefillArgs compiled in
   static constexpr bool kLoad = LOAD_;           // waves NCW.. load prepared T~/P (two-kernel path)
@@ -105,6 +105,10 @@ struct Variant {
   static constexpr int kStagers = NP_ - 3;
   static_assert(F * ROWS == 128 && NCW + NP <= 8, "unsupported launch variant");
   static_assert(NP == 4 || (!LOAD_ && NCW + NP == 8 && NCW <= 2), "pipelined producers fill the workgroup");
+  // One workgroup per CU runs a list of whole chains back to back
+  // (gdn_prefill_persistent_kernel); the four-producer F = 1 layout only.
+  static constexpr bool kPersist = PERSIST_;
+  static_assert(!PERSIST_ || (NCW_ == 4 && VT_ == 2 && NP_ == 4 && !LOAD_), "persistent: F = 1 only");
 };
 
 // Production launch variants by split factor F (workgroups per chain).  With F = 8
@@ -119,11 +123,14 @@ template <bool HOOKS>
 using SplitVariant4 = Variant<2, 1, HOOKS, false, 6>;
 template <bool HOOKS>
 using SplitVariant8 = Variant<1, 1, HOOKS, false, 7>;
+// F = 1 as one workgroup per CU running lists of chains (batches of many chains).
+template <bool HOOKS>
+using PersistVariant = Variant<4, 2, HOOKS, false, 4, true>;
 
 // The prep kernel of the two-kernel path: the four producer waves alone (no
 // consumers, no V staging); they copy each chunk's tiles out themselves (kCopy).
 struct PrepVariant {
-  static constexpr bool kHooks = false, kLoad = false, kCopy = true, kPipelined = false;
+  static constexpr bool kHooks = false, kLoad = false, kCopy = true, kPipelined = false, kPersist = false;
   static constexpr int NCW = 0, NP = 4, VT = 1, VW = 16, ROWS = 128, F = 1;
   static constexpr int NTHREADS = 64 * (NCW + 4);
   static constexpr int VSEG = 0;
@@ -135,6 +142,7 @@ struct PrepVariant {
 // (a sequence clamped into [0, T] has at most TC chunks).
 constexpr int kTileImage = 3 * C * TSTR / 8;
 constexpr int kMaxSortedSeqs = 1024;  // longest-first ordering up to this many sequences
+constexpr int kMaxPersistSeqs = 64;   // the persistent kernel serves batches of at most this many sequences
 
 struct __align__(16) PrefillSmem {
   static constexpr int kParities = 2;  // chunk buffers in flight
@@ -153,6 +161,13 @@ struct __align__(16) PrefillSmem {
   float eg[2][C];             // e^{gamma_c}
   float dd[2][C];             // e^{gamma_last - gamma_c}
   int seq;                    // sequence handled by this workgroup
+  int pseq[kMaxPersistSeqs];  // persistent kernel: the sequences of the workgroup's chains, in order,
+  int ps0[kMaxPersistSeqs];   // their token ranges [ps0, ps1),
+  int ps1[kMaxPersistSeqs];
+  int pcount;                 // and their number
+  int plen[kMaxPersistSeqs];  // persistent kernel: sequence lengths, starts and the longest-first
+  int pstart[kMaxPersistSeqs];  // order, for the list (formed while the first chain runs)
+  int porder[kMaxPersistSeqs];
   int sync[16];               // hand-off counters (enum SyncCounter)
   int spin_limit;             // kernels with testing hooks: polls before a hand-off wait gives up
   unsigned* aborts;           // kernels with testing hooks: optional count of waits that gave up
@@ -413,7 +428,8 @@ enum SyncCounter {
   kX32 = 6,       // off-diagonal block X32 stored
   kStaged = 7,    // pipelined: the chunk's K/Q staged and its gates stored (NS + 1 a chunk)
   kNRead = 8,     // pipelined: the left off-diagonal wave read its N operands
-  kVStaged = 9    // pipelined: the chunk's V staged (NS a chunk)
+  kVStaged = 9,   // pipelined: the chunk's V staged (NS a chunk)
+  kList = 10      // persistent kernel: the workgroup's chain list is complete (1)
 };
 constexpr int kSpinLimit = 1 << 21;  // default polls (about 70 ms) before a wait gives up
 
@@ -905,6 +921,14 @@ __device__ __forceinline__ void copy_tiles_out(const ChunkBufs& cb, u32x4* image
   }
 }
 
+// Persistent kernel: the first chain at or after position k of the workgroup's
+// list that has tokens (sm.pcount if none).
+template <class Smem>
+__device__ __forceinline__ int next_chain(Smem& sm, int k) {
+  while (k < sm.pcount && sm.ps1[k] <= sm.ps0[k]) ++k;
+  return k;
+}
+
 // The producer loop: chunk t is prepared into the buffers of parity t & 1 (of
 // Smem::kParities) once the consumers are done with the chunk that used them last
 // (chunk t - 2 with two parities).  The four producer waves meet twice per chunk
@@ -933,6 +957,19 @@ __device__ __forceinline__ void producer_loop(Smem& sm, const PrefillArgs& p, in
     voff[it] = c * p.Hv * D + 8 * sg;
   }
   static_assert(V::NP == 4 && !V::kPipelined, "pipelined producers run producer_loop_split");
+  // The persistent kernel runs the chains of the workgroup's list (chain k covers
+  // tokens [s0, s1)) as one stream of chunks; u counts the chunks of the stream and
+  // indexes the hand-offs and the buffer parities (u = t otherwise).
+  // Chain 0 (the longest of the list) is known before the rest of the list, which
+  // is waited for (kList) where the stream first looks past a chain.
+  int k = 0;
+  bool listed = false;
+  if constexpr (V::kPersist) {
+    s0 = sm.ps0[0];
+    s1 = sm.ps1[0];
+    nchunks = int((s1 - s0 + C - 1) / C);
+    if (nchunks == 0) return;  // the longest chain is empty: so are the others
+  }
   ProducerPrefetch f;
   uint4 fv[NVIT];
   producer_prefetch(p, s0, int(s1 - s0 < C ? s1 - s0 : C), h, hq, hk, pt, lo, f);
@@ -943,19 +980,37 @@ __device__ __forceinline__ void producer_loop(Smem& sm, const PrefillArgs& p, in
   PhaseClock clk;
   clk.start();
 
-  for (int t = 0; t < nchunks; ++t) {
+  int u = 0;
+  for (;;) {
+  for (int t = 0; t < nchunks; ++t, ++u) {
     // The lane index is re-materialised opaquely each tick so that lane-dependent
     // LDS addresses are recomputed in the loop rather than hoisted and spilled.
     int lane = lane0;
     asm volatile("" : "+v"(lane));
     const int64_t cs = s0 + int64_t(t) * C;
     const int clen = int(s1 - cs < C ? s1 - cs : C);
-    const int64_t ncs = cs + C;
-    const int nclen = int(s1 - ncs < C ? s1 - ncs : C);
-    const ChunkBufs cb = chunk_bufs(sm, t & 1);
-    // The buffers of chunk t - kParities (the same ones) consumed.
+    // The next chunk: this chain's, or (persistent) the next chain's first.
+    int64_t ncs = cs + C;
+    int nclen = int(s1 - ncs < C ? s1 - ncs : C);
+    bool has_next = ncs < s1;
+    if constexpr (V::kPersist) {
+      if (!has_next) {
+        if (!listed) {
+          wait_count<V::kHooks>(sm, kList, 1);
+          listed = true;
+        }
+        const int nk = next_chain(sm, k + 1);
+        if (nk < sm.pcount) {
+          has_next = true;
+          ncs = sm.ps0[nk];
+          nclen = int(sm.ps1[nk] - ncs < C ? sm.ps1[nk] - ncs : C);
+        }
+      }
+    }
+    const ChunkBufs cb = chunk_bufs(sm, u & 1);
+    // The buffers of chunk u - kParities (the same ones) consumed.
     constexpr int kPar = Smem::kParities;
-    if (t >= kPar) wait_count<V::kHooks>(sm, kConsumed, V::NCW * (t - kPar + 1));
+    if (u >= kPar) wait_count<V::kHooks>(sm, kConsumed, V::NCW * (u - kPar + 1));
     if constexpr (V::kCopy) {
       if (t >= 1) {
         wait_count<V::kHooks>(sm, kReady, 4 * t);  // chunk t - 1 handed over by all four waves
@@ -979,7 +1034,7 @@ __device__ __forceinline__ void producer_loop(Smem& sm, const PrefillArgs& p, in
     }
     clk.lap(1);
     signal_count(sm, kPPhase, lane);
-    wait_count<V::kHooks>(sm, kPPhase, 4 * (2 * t + 1));  // all of K/Q/gates staged
+    wait_count<V::kHooks>(sm, kPPhase, 4 * (2 * u + 1));  // all of K/Q/gates staged
     clk.lap(2);
     // The rest of the chunk is the longer chain: producer waves go ahead of the
     // consumer wave sharing the SIMD.
@@ -993,14 +1048,14 @@ __device__ __forceinline__ void producer_loop(Smem& sm, const PrefillArgs& p, in
     // other waves issue their loads after their diagonal tile, the solve wave
     // after its solve.
     constexpr bool kSolveFirst = V::F > 1;
-    if (!kSolveFirst && ncs < s1) producer_prefetch(p, ncs, nclen, h, hq, hk, pt, lo, f);
+    if (!kSolveFirst && has_next) producer_prefetch(p, ncs, nclen, h, hq, hk, pt, lo, f);
     clk.lap(10);
     switch (pw) {
       case 0:
         diag_tiles<0, 1>(sm, cb, lane);
         signal_count(sm, kDiagN, lane);
         clk.lap(3);
-        wait_count<V::kHooks>(sm, kDiagN, 4 * (t + 1));
+        wait_count<V::kHooks>(sm, kDiagN, 4 * (u + 1));
         clk.lap(4);
         diag_solve(sm, cb, lane);
         clk.lap(5);
@@ -1008,7 +1063,7 @@ __device__ __forceinline__ void producer_loop(Smem& sm, const PrefillArgs& p, in
       case 1: {
         diag_tiles<1, 2>(sm, cb, lane);
         signal_count(sm, kDiagN, lane);
-        if (kSolveFirst && ncs < s1) producer_prefetch(p, ncs, nclen, h, hq, hk, pt, lo, f);
+        if (kSolveFirst && has_next) producer_prefetch(p, ncs, nclen, h, hq, hk, pt, lo, f);
         const TileJob j1[2] = {{1, 1, 0}, {1, 2, 0}};
         run_tiles(sm, cb, j1, p.scale, lane);
         const TileJob j2[2] = {{2, 0, 0}, {2, 3, 3}};
@@ -1018,7 +1073,7 @@ __device__ __forceinline__ void producer_loop(Smem& sm, const PrefillArgs& p, in
       case 2: {
         diag_tiles<2, 3>(sm, cb, lane);
         signal_count(sm, kDiagN, lane);
-        if (kSolveFirst && ncs < s1) producer_prefetch(p, ncs, nclen, h, hq, hk, pt, lo, f);
+        if (kSolveFirst && has_next) producer_prefetch(p, ncs, nclen, h, hq, hk, pt, lo, f);
         const TileJob j1[2] = {{1, 3, 0}, {1, 2, 1}};
         run_tiles(sm, cb, j1, p.scale, lane);
         const TileJob j2[2] = {{2, 1, 0}, {2, 3, 0}};
@@ -1028,7 +1083,7 @@ __device__ __forceinline__ void producer_loop(Smem& sm, const PrefillArgs& p, in
       default: {
         diag_tiles<3, 4>(sm, cb, lane);
         signal_count(sm, kDiagN, lane);
-        if (kSolveFirst && ncs < s1) producer_prefetch(p, ncs, nclen, h, hq, hk, pt, lo, f);
+        if (kSolveFirst && has_next) producer_prefetch(p, ncs, nclen, h, hq, hk, pt, lo, f);
         const TileJob j1[2] = {{1, 3, 1}, {1, 3, 2}};
         run_tiles(sm, cb, j1, p.scale, lane);
         const TileJob j2[2] = {{2, 1, 1}, {2, 2, 0}};
@@ -1038,21 +1093,21 @@ __device__ __forceinline__ void producer_loop(Smem& sm, const PrefillArgs& p, in
     }
     clk.lap(3);
     signal_count(sm, kPPhase, lane);
-    wait_count<V::kHooks>(sm, kPPhase, 4 * (2 * t + 2));  // diagonal blocks and N tiles done
+    wait_count<V::kHooks>(sm, kPPhase, 4 * (2 * u + 2));  // diagonal blocks and N tiles done
     clk.lap(6);
 
     // 3: off-diagonal blocks of T~ (waves 1 and 3), the remaining P tiles (two
     // each on waves 0 and 2), V once the consumers have read the previous chunk's
     switch (pw) {
       case 0: {
-        if (kSolveFirst && ncs < s1) producer_prefetch(p, ncs, nclen, h, hq, hk, pt, lo, f);
+        if (kSolveFirst && has_next) producer_prefetch(p, ncs, nclen, h, hq, hk, pt, lo, f);
         const TileJob j1[2] = {{2, 2, 1}, {2, 2, 2}};
         run_tiles(sm, cb, j1, p.scale, lane);
-        if (ncs < s1) gts = chunk_gates(f, lane, nclen, neg_decay, dt_bias);  // chunk t + 1's gates
+        if (has_next) gts = chunk_gates(f, lane, nclen, neg_decay, dt_bias);  // the next chunk's gates
         break;
       }
       case 1: {
-        offdiag_right(sm, cb, t, lane);
+        offdiag_right(sm, cb, u, lane);
         break;
       }
       case 2: {
@@ -1061,11 +1116,11 @@ __device__ __forceinline__ void producer_loop(Smem& sm, const PrefillArgs& p, in
         break;
       }
       default:
-        offdiag_left<V::kHooks>(sm, cb, t, lane);
+        offdiag_left<V::kHooks>(sm, cb, u, lane);
         break;
     }
     clk.lap(7);
-    if (t >= 1) wait_count<V::kHooks>(sm, kVFree, V::NCW * t);
+    if (u >= 1) wait_count<V::kHooks>(sm, kVFree, V::NCW * u);
     clk.lap(8);
 #pragma unroll
     for (int it = 0; it < NVIT; ++it) {
@@ -1076,6 +1131,16 @@ __device__ __forceinline__ void producer_loop(Smem& sm, const PrefillArgs& p, in
     __builtin_amdgcn_s_setprio(0);
     if (!V::kHooks || p.ready_chunks <= 0 || t < p.ready_chunks) signal_count(sm, kReady, lane);
     clk.lap(9);
+  }
+  if constexpr (!V::kPersist) {
+    break;
+  } else {
+    k = next_chain(sm, k + 1);
+    if (k >= sm.pcount) break;
+    s0 = sm.ps0[k];
+    s1 = sm.ps1[k];
+    nchunks = int((s1 - s0 + C - 1) / C);
+  }
   }
   if constexpr (V::kCopy) {
     wait_count<V::kHooks>(sm, kReady, 4 * nchunks);
@@ -1489,7 +1554,7 @@ __device__ __forceinline__ int vrow(int vt, int n) {
 template <class V>
 __device__ __forceinline__ void consumer_loop(PrefillSmem& sm, const PrefillArgs& p, int64_t s0, int64_t s1,
                                               int nchunks, int h, int row0, int wave, int lane0,
-                                              f32x4 (&S)[V::VT][8]) {
+                                              f32x4 (&S)[V::VT][8], int u0 = 0) {
   constexpr int VT = V::VT, VW = V::VW;
   const int64_t vstride = int64_t(p.Hv) * D;
   // Element offset of output row 16ct + lane%16, first column of the lane's output
@@ -1506,14 +1571,17 @@ __device__ __forceinline__ void consumer_loop(PrefillSmem& sm, const PrefillArgs
     const int g = lane >> 4, n16 = lane & 15;
     const int64_t cs = s0 + int64_t(t - 1) * C;
     const int clen = int(s1 - cs < C ? s1 - cs : C);
-    const ChunkBufs cb = chunk_bufs(sm, (t - 1) & 1);
+    // u: the chunk's position in the workgroup's stream of chunks (persistent
+    // kernel: u0 chunks of earlier chains precede this chain's).
+    const int u = u0 + t;
+    const ChunkBufs cb = chunk_bufs(sm, (u - 1) & 1);
     if constexpr (V::kPipelined) {
       // Pipelined producers hand a chunk over in two steps: K, Q, the gates and V for
       // the retrieve and Y, then T~ and P ("ready", below) for v_new and the output.
-      wait_count<V::kHooks>(sm, kStaged, (V::kStagers + 1) * t);
-      wait_count<V::kHooks>(sm, kVStaged, V::kStagers * t);
+      wait_count<V::kHooks>(sm, kStaged, (V::kStagers + 1) * u);
+      wait_count<V::kHooks>(sm, kVStaged, V::kStagers * u);
     } else {
-      wait_count<V::kHooks>(sm, kReady, 4 * t);  // chunk t - 1 prepared
+      wait_count<V::kHooks>(sm, kReady, 4 * u);  // chunk u - 1 prepared
     }
     clk.lap(0);
 
@@ -1543,7 +1611,7 @@ __device__ __forceinline__ void consumer_loop(PrefillSmem& sm, const PrefillArgs
       for (int vt = 0; vt < VT; ++vt) Xq[vt][ct] = Xq[vt][ct] * ecn;
     }
     signal_count(sm, kVFree, lane);  // V of this chunk read
-    if constexpr (V::kPipelined) wait_count<V::kHooks>(sm, kReady, (V::kStagers + 2) * t);  // T~ and P
+    if constexpr (V::kPipelined) wait_count<V::kHooks>(sm, kReady, (V::kStagers + 2) * u);  // T~ and P
     clk.lap(2);
     // The 16-row consumer reads all its T~ and P operands now (they are ready), so that
     // their latency overlaps the Y split; the 32-row one, short of registers, as used.
@@ -1836,6 +1904,193 @@ __global__ __launch_bounds__(V::NTHREADS) void gdn_prefill_kernel(PrefillArgs p)
   }
 }
 
+// Minimum over the wave (uniform): DPP within each row of 16 lanes, then the four
+// row minima.
+__device__ __forceinline__ uint32_t wave_min(uint32_t x) {
+  x = min(x, uint32_t(__builtin_amdgcn_update_dpp(0, int(x), 0xB1, 0xF, 0xF, false)));
+  x = min(x, uint32_t(__builtin_amdgcn_update_dpp(0, int(x), 0x4E, 0xF, 0xF, false)));
+  x = min(x, uint32_t(__builtin_amdgcn_update_dpp(0, int(x), 0x124, 0xF, 0xF, false)));
+  x = min(x, uint32_t(__builtin_amdgcn_update_dpp(0, int(x), 0x128, 0xF, 0xF, false)));
+  const uint32_t a = uint32_t(__builtin_amdgcn_readlane(int(x), 0)), b = uint32_t(__builtin_amdgcn_readlane(int(x), 16));
+  const uint32_t c = uint32_t(__builtin_amdgcn_readlane(int(x), 32)), d = uint32_t(__builtin_amdgcn_readlane(int(x), 48));
+  return min(min(a, b), min(c, d));
+}
+
+// Persistent form of the F = 1 kernel, for batches of more chains than CUs: one
+// workgroup per CU runs a list of whole chains back to back, so that the next
+// chain's first chunk is loaded and prepared while the consumers finish the current
+// one (a workgroup per chain pays for that, its start-up and its drain once per
+// chain: about three chunk times).  The grid is B = gridDim.x / Hv bins of Hv
+// workgroups; workgroup (bin, i) runs v-head h(i) of every sequence of its bin.
+// Every workgroup forms the same longest-processing-time schedule of the
+// sequences over the bins (longest first, each onto the least-loaded bin; cost 3
+// per chunk + 2 per sequence, ties to the lower bin), so all heads of a sequence
+// share one bin and a bin's workgroups share their list.
+template <class V>
+__global__ __launch_bounds__(V::NTHREADS) void gdn_prefill_persistent_kernel(PrefillArgs p) {
+  static_assert(V::kPersist && V::NCW == 4 && V::VT == 2, "persistent kernel: Variant<4, 2, ..., true>");
+  constexpr int NCW = V::NCW, VT = V::VT, VW = V::VW, NTHREADS = V::NTHREADS;
+  __shared__ PrefillSmem sm;
+
+  const int tid = threadIdx.x;
+  const int lane0 = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int bid = blockIdx.x;
+  const int nbins = int(gridDim.x) / p.Hv, bin = bid / p.Hv, i = bid % p.Hv;
+  // Workgroups are dealt to the 8 XCDs round-robin: with Hv a multiple of 16,
+  // workgroups i and i + 8 of a bin (one XCD) take the GQA pair 2j, 2j + 1.
+  const int h = p.Hv % 16 == 0 ? (i & ~15) | ((i & 7) << 1) | ((i >> 3) & 1) : i;
+  const int hq = h / (p.Hv / p.Hq);
+  const int hk = h / (p.Hv / p.Hk);
+
+  // Sequence lengths and starts, then the longest-first order (ties: lower index).
+  // Chain 0 of bin b is the sequence of rank b: the schedule below places the
+  // first B sequences one per bin, in order.
+  for (int s = tid; s < p.N; s += NTHREADS) {
+    int64_t a = load_cu(p.cu_seqlens, p.cu_is_64, s), b = load_cu(p.cu_seqlens, p.cu_is_64, s + 1);
+    a = a < 0 ? 0 : (a > p.T ? p.T : a);
+    b = b < a ? a : (b > p.T ? p.T : b);
+    sm.plen[s] = int(b - a);
+    sm.pstart[s] = int(a);
+  }
+  // Blocks of T~, N and P that are never written per chunk are read as zeros.
+  {
+    const uint4 z = uint4{0u, 0u, 0u, 0u};
+    for (int e = tid; e < C * TSTR / 8; e += NTHREADS) {
+      reinterpret_cast<uint4*>(sm.P[0])[e] = z;
+      reinterpret_cast<uint4*>(sm.P[1])[e] = z;
+      reinterpret_cast<uint4*>(sm.Th[0])[e] = z;
+      reinterpret_cast<uint4*>(sm.Th[1])[e] = z;
+      reinterpret_cast<uint4*>(sm.Tl[0])[e] = z;
+      reinterpret_cast<uint4*>(sm.Tl[1])[e] = z;
+      if (e < NROWS * TSTR / 8) {
+        reinterpret_cast<uint4*>(sm.Nh)[e] = z;
+        reinterpret_cast<uint4*>(sm.Nl)[e] = z;
+      }
+    }
+    if (tid < 16) sm.sync[tid] = 0;
+    if (V::kHooks && tid == 0) {
+      sm.spin_limit = p.spin_limit > 0 ? p.spin_limit : kSpinLimit;
+      sm.aborts = p.aborts;
+    }
+  }
+  __syncthreads();
+  for (int s = tid; s < p.N; s += NTHREADS) {
+    const int ls = sm.plen[s];
+    int r = 0;
+    for (int j = 0; j < p.N; ++j) {
+      const int lj = sm.plen[j];
+      r += (lj > ls) | ((lj == ls) & (j < s));
+    }
+    sm.porder[r] = s;
+    if (r == bin) {
+      sm.pseq[0] = s;
+      sm.ps0[0] = sm.pstart[s];
+      sm.ps1[0] = sm.pstart[s] + ls;
+    }
+  }
+  __syncthreads();  // chain 0, cleared LDS and counters visible to both roles
+
+  if (wave >= NCW) {
+    producer_loop<V>(sm, p, 0, 0, 0, h, hq, hk, 0, wave - NCW, lane0);
+    return;
+  }
+
+  if (wave == 0) {
+    // The rest of the list, while the producers prepare chain 0's first chunk:
+    // longest-processing-time over the bins.  Lane r holds the cost of the
+    // sequence of rank r; lane b < B (at most 64) holds bin b's load.
+    const int sr = lane0 < p.N ? sm.porder[lane0] : 0;
+    const int lr = lane0 < p.N ? sm.plen[sr] : 0;
+    const int cost_r = 3 * (lr / C + (lr % C != 0)) + 2;
+    uint32_t load = lane0 < nbins ? 0u : 0xffffffffu;
+    int cnt = 0;
+    for (int r = 0; r < p.N; ++r) {
+      const uint32_t m = wave_min(load);
+      const int b = __builtin_ctzll(__ballot(load == m));
+      if (lane0 == b) load += uint32_t(__builtin_amdgcn_readlane(cost_r, r));
+      if (b == bin) {
+        if (lane0 == r) {
+          sm.pseq[cnt] = sr;
+          sm.ps0[cnt] = sm.pstart[sr];
+          sm.ps1[cnt] = sm.pstart[sr] + lr;
+        }
+        ++cnt;
+      }
+    }
+    if (lane0 == 0) sm.pcount = cnt;
+    signal_count(sm, kList, lane0);
+  }
+
+  // Consumers: state rows v = VW*wave + vrow(vt, n16), cols k = 16*kt + 4g + i.
+  const int g = lane0 >> 4, n16 = lane0 & 15;
+  int nchains = 1;
+  int u0 = 0;
+  for (int k = 0; k < nchains; ++k) {
+    const int seq = sm.pseq[k];
+    const int64_t s0 = sm.ps0[k], s1 = sm.ps1[k];
+    const int nchunks = int((s1 - s0 + C - 1) / C);
+    const int64_t state_head = (int64_t(seq) * p.Hv + h) * D * D;
+    f32x4 S[VT][8];
+#pragma unroll
+    for (int vt = 0; vt < VT; ++vt) {
+      const int v = VW * wave + vrow<VT>(vt, n16);
+#pragma unroll
+      for (int kt = 0; kt < 8; ++kt) {
+        if (p.state) {
+          const float4 x = *reinterpret_cast<const float4*>(p.state + state_head + int64_t(v) * D + 16 * kt + 4 * g);
+          S[vt][kt] = f32x4{x.x, x.y, x.z, x.w};
+        } else {
+          S[vt][kt] = zero4();
+        }
+      }
+    }
+    if (nchunks > 0) {
+      consumer_loop<V>(sm, p, s0, s1, nchunks, h, 0, wave, lane0, S, u0);
+      u0 += nchunks;
+    }
+    // Final state (for an empty sequence: the initial state, or zeros).
+    if (nchunks > 0 || p.state != p.new_state) {
+#pragma unroll
+      for (int vt = 0; vt < VT; ++vt) {
+        const int v = VW * wave + vrow<VT>(vt, n16);
+#pragma unroll
+        for (int kt = 0; kt < 8; ++kt) {
+          const f32x4 x = S[vt][kt];
+          *reinterpret_cast<float4*>(p.new_state + state_head + int64_t(v) * D + 16 * kt + 4 * g) =
+              make_float4(x[0], x[1], x[2], x[3]);
+        }
+      }
+    }
+    if (k == 0) {
+      wait_count<V::kHooks>(sm, kList, 1);  // the rest of the list
+      nchains = sm.pcount;
+    }
+  }
+  if (aborted(sm)) {
+    // A hand-off wait gave up: NaN over every output element and state element of
+    // this wave's rows, in every chain of the workgroup.
+    const int64_t vstride = int64_t(p.Hv) * D;
+    for (int k = 0; k < nchains; ++k) {
+      const int seq = sm.pseq[k];
+      const int64_t s0 = sm.ps0[k], s1 = sm.ps1[k];
+      uint16_t* obase = p.out + int64_t(h) * D + VW * wave + 8 * (lane0 >> 4);
+      for (int64_t tok = s0 + n16; tok < s1; tok += 16)
+        *reinterpret_cast<uint4*>(obase + tok * vstride) = uint4{kNaNx2, kNaNx2, kNaNx2, kNaNx2};
+      const int64_t state_head = (int64_t(seq) * p.Hv + h) * D * D;
+      const float nan = __builtin_nanf("");
+#pragma unroll
+      for (int vt = 0; vt < VT; ++vt) {
+        const int v = VW * wave + vrow<VT>(vt, n16);
+#pragma unroll
+        for (int kt = 0; kt < 8; ++kt)
+          *reinterpret_cast<float4*>(p.new_state + state_head + int64_t(v) * D + 16 * kt + 4 * g) =
+              make_float4(nan, nan, nan, nan);
+      }
+    }
+  }
+}
+
 // Prep kernel of the two-kernel path (few chains).  Workgroup b = (s R' + r) Hv + h
 // prepares chunks r p.prep_chunks .. (r + 1) p.prep_chunks - 1 of sequence s for
 // v-head h (R' = ceil(TC / p.prep_chunks)): the producer waves run their loop over
@@ -1890,6 +2145,21 @@ hipError_t launch_variant(const PrefillArgs& a, hipStream_t stream) {
   const int64_t chains = int64_t(a.N) * a.Hv;
   const int64_t grid = V::F == 1 ? (chains + 15) / 16 * 16 : (chains + 7) / 8 * 8 * V::F;
   hipLaunchKernelGGL(gdn_prefill_kernel<V>, dim3(unsigned(grid)), dim3(V::NTHREADS), 0, stream, a);
+  return hipGetLastError();
+}
+
+int device_cus();
+
+// Batches of more chains than CUs run persistently where they can: a workgroup per
+// CU, Hv dividing the CUs into at most 64 bins, at most kMaxPersistSeqs sequences.
+bool persistent_batch(const PrefillArgs& a) {
+  const int cus = device_cus();
+  return a.N <= kMaxPersistSeqs && cus % a.Hv == 0 && cus / a.Hv <= 64 && int64_t(a.N) * a.Hv > cus;
+}
+
+template <class V>
+hipError_t launch_persistent(const PrefillArgs& a, hipStream_t stream) {
+  hipLaunchKernelGGL(gdn_prefill_persistent_kernel<V>, dim3(unsigned(device_cus())), dim3(V::NTHREADS), 0, stream, a);
   return hipGetLastError();
 }
 
@@ -2004,6 +2274,7 @@ hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream) {
   // Launches that use the testing hooks get kernels with the hooks compiled in;
   // production launches keep them out of the device code.
   if (a.spin_limit != 0 || a.ready_chunks != 0 || a.aborts != nullptr) {
+    if (persistent_batch(a)) return launch_persistent<PersistVariant<true>>(a, stream);
     switch (F) {
       case 1: return launch_variant<SplitVariant1<true>>(a, stream);
       case 2: return launch_variant<SplitVariant2<true>>(a, stream);
@@ -2030,6 +2301,7 @@ hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream) {
   // Split chains use 16-row consumer waves (VT = 1), whose per-chunk chain is
   // shorter than a 32-row wave's.  Unsplit chains (F = 1) keep four 32-row waves:
   // eight 16-row waves and the four producers would exceed the register file.
+  if (persistent_batch(a)) return launch_persistent<PersistVariant<false>>(a, stream);
   switch (F) {
     case 1: return launch_variant<SplitVariant1<false>>(a, stream);
     case 2: return launch_variant<SplitVariant2<false>>(a, stream);

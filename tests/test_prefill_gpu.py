@@ -486,3 +486,82 @@ def test_prefill_max_heads(gpu):
     o_ref, s_ref = oracle_prefill(_heads_of(p, idx))
     assert_close(host(out[:, idx.to(gpu)]), o_ref, OUT_RTOL, OUT_ATOL, "output")
     assert_close(host(ns[:, idx.to(gpu)]), s_ref, STATE_RTOL, STATE_ATOL, "new_state")
+
+
+def _persistent_lengths():
+    rng = np.random.default_rng(77)
+    return [0, 1, 63, 64, 65, 128, 129] + [int(x) for x in rng.integers(1, 300, 33)]
+
+
+PERSISTENT_BATCHES = {
+    # 40 sequences (zero, one and chunk-boundary lengths among them) of 8 v-heads:
+    # 320 chains over 32 bins of 8 workgroups; no initial states
+    "hv8_ragged": (_persistent_lengths(), Heads(4, 4, 8), False, False, torch.int32),
+    # 64 sequences of 100 tokens, 32 v-heads: 2,048 chains over 8 bins, state
+    # updated in place, int64 cu_seqlens
+    "hv32_many_in_place": ([100] * 64, Heads(16, 16, 32), True, True, torch.int64),
+    # 12 sequences, the 5 shortest empty: the bin whose first chain is empty, and an
+    # empty chain after a non-empty one in another bin's list
+    "empty_chains": ([300, 250, 200, 150, 100, 70, 65, 0, 0, 0, 0, 0], Heads(16, 16, 32), True, False,
+                     torch.int32),
+}
+
+
+@pytest.mark.parametrize("case", list(PERSISTENT_BATCHES))
+def test_prefill_persistent_batches(gpu, case):
+    """Batches of more (sequence, v-head) chains than CUs (at most 64 sequences, Hv
+    dividing the CU count) run one workgroup per CU, each through a list of chains.
+    Every output and final state against the oracle; three sequences run alone (a
+    split launch) give the packed results bit for bit."""
+    lens, heads, with_state, in_place, cu_dtype = PERSISTENT_BATCHES[case]
+    say(f"prefill persistent batch {case}: {len(lens)} sequences, heads {heads}")
+    p = workloads.prefill_inputs(lens, heads, seed=len(lens), gate="slow", state_scale=0.5,
+                                 with_state=with_state, cu_dtype=cu_dtype)
+    assert len(lens) * heads.hv > 256
+    o_ref, s_ref = oracle_prefill(p)
+    out, ns = run_prefill(p, gpu, in_place=in_place)
+    torch.cuda.synchronize()
+    assert_close(host(out), o_ref, OUT_RTOL, OUT_ATOL, "output")
+    assert_close(host(ns), s_ref, STATE_RTOL, STATE_ATOL, "new_state")
+    cu = p["cu_seqlens"].tolist()
+    for i in (int(np.argmax(lens)), len(lens) // 2, len(lens) - 1):
+        s, e = cu[i], cu[i + 1]
+        sub = {k: (p[k][s:e] if k in ("q", "k", "v", "a", "b") else p[k])
+               for k in ("q", "k", "v", "a", "b", "A_log", "dt_bias", "scale")}
+        sub["state"] = None if p["state"] is None else p["state"][i:i + 1]
+        sub["cu_seqlens"] = torch.tensor([0, e - s], dtype=torch.int32)
+        o1, s1 = run_prefill(sub, gpu)
+        torch.cuda.synchronize()
+        assert torch.equal(o1, out[s:e]) and torch.equal(s1[0], ns[i]), f"seq {i} packed != alone"
+
+
+@pytest.mark.giveups_expected
+def test_prefill_persistent_bounded_waits(gpu):
+    """The hand-off failure path of the persistent kernel, forced from the host: 12
+    sequences of 2-5 chunks, 32 v-heads (384 chains, one workgroup per CU).  With the
+    producers signalling only the first chunk of each chain and a 2,000-poll limit,
+    each workgroup's first chain has a consumer wait that can only give up: the launch
+    completes, the give-ups are counted by the hook counter and the device counter,
+    every output and final state is NaN, and the next normal launch is exact again."""
+    lens = [300, 257, 200, 190, 150, 140, 129, 100, 90, 80, 70, 65]
+    p = workloads.prefill_inputs(lens, Heads(16, 16, 32), seed=22, gate="slow", state_scale=0.5)
+    binding.prefill_giveups(reset=True)
+    say("prefill persistent bounded waits: hooks off")
+    o0, s0, a0 = _prefill_fault_injection(p, gpu, 0, 0)
+    o1, s1 = run_prefill(p, gpu)
+    torch.cuda.synchronize()
+    assert int(a0.item()) == 0 and binding.prefill_giveups() == 0
+    assert torch.equal(o0, o1) and torch.equal(s0, s1)
+    say("prefill persistent bounded waits: chunk-ready signals stop after each chain's chunk 0")
+    o2, s2, a2 = _prefill_fault_injection(p, gpu, 2000, 1)
+    torch.cuda.synchronize()
+    n = int(a2.item())
+    cus = torch.cuda.get_device_properties(gpu).multi_processor_count
+    assert cus < 12 * 32 and cus <= n <= cus * 8, (n, cus)
+    assert binding.prefill_giveups(reset=True) == n, "the device counter must see every give-up"
+    assert torch.isnan(o2.float()).all() and torch.isnan(s2).all()
+    say("prefill persistent bounded waits: a normal launch afterwards")
+    o3, s3 = run_prefill(p, gpu)
+    torch.cuda.synchronize()
+    assert torch.equal(o3, o1) and torch.equal(s3, s1)
+    assert binding.prefill_giveups() == 0
