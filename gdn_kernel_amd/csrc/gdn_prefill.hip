@@ -142,7 +142,8 @@ struct PrepVariant {
 // (a sequence clamped into [0, T] has at most TC chunks).
 constexpr int kTileImage = 3 * C * TSTR / 8;
 constexpr int kMaxSortedSeqs = 1024;  // longest-first ordering up to this many sequences
-constexpr int kMaxPersistSeqs = 64;   // the persistent kernel serves batches of at most this many sequences
+constexpr int kMaxPersistList = 128;  // chains per workgroup of the persistent kernel
+constexpr int kMaxPersistLpt = 64;    // batches of at most this many sequences get a longest-processing-time list
 
 struct __align__(16) PrefillSmem {
   static constexpr int kParities = 2;  // chunk buffers in flight
@@ -161,13 +162,13 @@ struct __align__(16) PrefillSmem {
   float eg[2][C];             // e^{gamma_c}
   float dd[2][C];             // e^{gamma_last - gamma_c}
   int seq;                    // sequence handled by this workgroup
-  int pseq[kMaxPersistSeqs];  // persistent kernel: the sequences of the workgroup's chains, in order,
-  int ps0[kMaxPersistSeqs];   // their token ranges [ps0, ps1),
-  int ps1[kMaxPersistSeqs];
+  int pseq[kMaxPersistList];  // persistent kernel: the sequences of the workgroup's chains, in order,
+  int ps0[kMaxPersistList];   // their token ranges [ps0, ps1),
+  int ps1[kMaxPersistList];
   int pcount;                 // and their number
-  int plen[kMaxPersistSeqs];  // persistent kernel: sequence lengths, starts and the longest-first
-  int pstart[kMaxPersistSeqs];  // order, for the list (formed while the first chain runs)
-  int porder[kMaxPersistSeqs];
+  int plen[kMaxPersistLpt];   // persistent kernel, up to kMaxPersistLpt sequences: their lengths,
+  int pstart[kMaxPersistLpt];  // starts and longest-first order (the list is formed while the
+  int porder[kMaxPersistLpt];  // first chain runs)
   int sync[16];               // hand-off counters (enum SyncCounter)
   int spin_limit;             // kernels with testing hooks: polls before a hand-off wait gives up
   unsigned* aborts;           // kernels with testing hooks: optional count of waits that gave up
@@ -959,9 +960,9 @@ __device__ __forceinline__ void producer_loop(Smem& sm, const PrefillArgs& p, in
   static_assert(V::NP == 4 && !V::kPipelined, "pipelined producers run producer_loop_split");
   // The persistent kernel runs the chains of the workgroup's list (chain k covers
   // tokens [s0, s1)) as one stream of chunks; u counts the chunks of the stream and
-  // indexes the hand-offs and the buffer parities (u = t otherwise).
-  // Chain 0 (the longest of the list) is known before the rest of the list, which
-  // is waited for (kList) where the stream first looks past a chain.
+  // indexes the hand-offs and the buffer parities (u = t otherwise).  Chain 0
+  // (the longest of the list) is known before the rest of the list, which is
+  // waited for (kList) where the stream first looks past a chain.
   int k = 0;
   bool listed = false;
   if constexpr (V::kPersist) {
@@ -1926,7 +1927,7 @@ __device__ __forceinline__ uint32_t wave_min(uint32_t x) {
 // sequences over the bins (longest first, each onto the least-loaded bin; cost 3
 // per chunk + 2 per sequence, ties to the lower bin), so all heads of a sequence
 // share one bin and a bin's workgroups share their list.
-template <class V>
+template <class V, bool LPT>
 __global__ __launch_bounds__(V::NTHREADS) void gdn_prefill_persistent_kernel(PrefillArgs p) {
   static_assert(V::kPersist && V::NCW == 4 && V::VT == 2, "persistent kernel: Variant<4, 2, ..., true>");
   constexpr int NCW = V::NCW, VT = V::VT, VW = V::VW, NTHREADS = V::NTHREADS;
@@ -1943,15 +1944,21 @@ __global__ __launch_bounds__(V::NTHREADS) void gdn_prefill_persistent_kernel(Pre
   const int hq = h / (p.Hv / p.Hq);
   const int hk = h / (p.Hv / p.Hk);
 
-  // Sequence lengths and starts, then the longest-first order (ties: lower index).
-  // Chain 0 of bin b is the sequence of rank b: the schedule below places the
-  // first B sequences one per bin, in order.
+  // Sequence lengths and starts, then the longest-first order (ties: lower index):
+  // for a longest-processing-time list (at most kMaxPersistLpt sequences) in LDS
+  // arrays of their own, which consumer wave 0 reads while the first chain runs;
+  // for more sequences in the V tile (scratch until the producers stage the first
+  // chunk's V).  Chain 0 of bin b is the sequence of rank b either way.
+  constexpr bool lpt = LPT;  // p.N <= kMaxPersistLpt
+  int* plen = lpt ? sm.plen : reinterpret_cast<int*>(sm.V);
+  int* pstart = lpt ? sm.pstart : plen + kMaxSortedSeqs;
+  int* porder = lpt ? sm.porder : pstart + kMaxSortedSeqs;
   for (int s = tid; s < p.N; s += NTHREADS) {
     int64_t a = load_cu(p.cu_seqlens, p.cu_is_64, s), b = load_cu(p.cu_seqlens, p.cu_is_64, s + 1);
     a = a < 0 ? 0 : (a > p.T ? p.T : a);
     b = b < a ? a : (b > p.T ? p.T : b);
-    sm.plen[s] = int(b - a);
-    sm.pstart[s] = int(a);
+    plen[s] = int(b - a);
+    pstart[s] = int(a);
   }
   // Blocks of T~, N and P that are never written per chunk are read as zeros.
   {
@@ -1976,32 +1983,51 @@ __global__ __launch_bounds__(V::NTHREADS) void gdn_prefill_persistent_kernel(Pre
   }
   __syncthreads();
   for (int s = tid; s < p.N; s += NTHREADS) {
-    const int ls = sm.plen[s];
+    const int ls = plen[s];
     int r = 0;
     for (int j = 0; j < p.N; ++j) {
-      const int lj = sm.plen[j];
+      const int lj = plen[j];
       r += (lj > ls) | ((lj == ls) & (j < s));
     }
-    sm.porder[r] = s;
+    porder[r] = s;
     if (r == bin) {
       sm.pseq[0] = s;
-      sm.ps0[0] = sm.pstart[s];
-      sm.ps1[0] = sm.pstart[s] + ls;
+      sm.ps0[0] = pstart[s];
+      sm.ps1[0] = pstart[s] + ls;
     }
   }
-  __syncthreads();  // chain 0, cleared LDS and counters visible to both roles
+  if constexpr (!lpt) {
+    __syncthreads();  // porder complete
+    // Many sequences: boustrophedon over the longest-first order.  Round j of B
+    // ranks gives rank jB + b (j even) or jB + B - 1 - b (j odd) to bin b.
+    const int cnt = p.N / nbins + (p.N % nbins > (p.N / nbins % 2 == 0 ? bin : nbins - 1 - bin));
+    for (int j = 1 + tid; j < cnt; j += NTHREADS) {
+      const int r = j * nbins + (j % 2 == 0 ? bin : nbins - 1 - bin);
+      const int sj = porder[r];
+      sm.pseq[j] = sj;
+      sm.ps0[j] = pstart[sj];
+      sm.ps1[j] = pstart[sj] + plen[sj];
+    }
+    if (tid == 0) {
+      sm.pcount = cnt;
+      sm.sync[kList] = 1;
+    }
+  }
+  __syncthreads();  // chain 0 (with more sequences, the whole list), cleared LDS and counters
 
   if (wave >= NCW) {
     producer_loop<V>(sm, p, 0, 0, 0, h, hq, hk, 0, wave - NCW, lane0);
     return;
   }
 
-  if (wave == 0) {
+  if (lpt && wave == 0) {
     // The rest of the list, while the producers prepare chain 0's first chunk:
-    // longest-processing-time over the bins.  Lane r holds the cost of the
+    // longest-processing-time over the bins, longest first, each sequence onto the
+    // least-loaded bin (cost 3 per chunk + 2 per sequence; ties to the lower bin;
+    // the first B sequences go one per bin, in order).  Lane r holds the cost of the
     // sequence of rank r; lane b < B (at most 64) holds bin b's load.
-    const int sr = lane0 < p.N ? sm.porder[lane0] : 0;
-    const int lr = lane0 < p.N ? sm.plen[sr] : 0;
+    const int sr = lane0 < p.N ? porder[lane0] : 0;
+    const int lr = lane0 < p.N ? plen[sr] : 0;
     const int cost_r = 3 * (lr / C + (lr % C != 0)) + 2;
     uint32_t load = lane0 < nbins ? 0u : 0xffffffffu;
     int cnt = 0;
@@ -2010,10 +2036,10 @@ __global__ __launch_bounds__(V::NTHREADS) void gdn_prefill_persistent_kernel(Pre
       const int b = __builtin_ctzll(__ballot(load == m));
       if (lane0 == b) load += uint32_t(__builtin_amdgcn_readlane(cost_r, r));
       if (b == bin) {
-        if (lane0 == r) {
+        if (lane0 == r && cnt > 0) {
           sm.pseq[cnt] = sr;
-          sm.ps0[cnt] = sm.pstart[sr];
-          sm.ps1[cnt] = sm.pstart[sr] + lr;
+          sm.ps0[cnt] = pstart[sr];
+          sm.ps1[cnt] = pstart[sr] + lr;
         }
         ++cnt;
       }
@@ -2024,7 +2050,7 @@ __global__ __launch_bounds__(V::NTHREADS) void gdn_prefill_persistent_kernel(Pre
 
   // Consumers: state rows v = VW*wave + vrow(vt, n16), cols k = 16*kt + 4g + i.
   const int g = lane0 >> 4, n16 = lane0 & 15;
-  int nchains = 1;
+  int nchains = 1;  // chain 0 now; the rest of the list once it is complete
   int u0 = 0;
   for (int k = 0; k < nchains; ++k) {
     const int seq = sm.pseq[k];
@@ -2151,15 +2177,24 @@ hipError_t launch_variant(const PrefillArgs& a, hipStream_t stream) {
 int device_cus();
 
 // Batches of more chains than CUs run persistently where they can: a workgroup per
-// CU, Hv dividing the CUs into at most 64 bins, at most kMaxPersistSeqs sequences.
+// CU, Hv dividing the CUs into B <= 64 bins, at most kMaxSortedSeqs sequences and
+// kMaxPersistList per bin.
 bool persistent_batch(const PrefillArgs& a) {
   const int cus = device_cus();
-  return a.N <= kMaxPersistSeqs && cus % a.Hv == 0 && cus / a.Hv <= 64 && int64_t(a.N) * a.Hv > cus;
+  if (cus % a.Hv != 0 || cus / a.Hv > 64 || a.N > kMaxSortedSeqs || int64_t(a.N) * a.Hv <= cus) return false;
+  const int bins = cus / a.Hv;
+  return (a.N + bins - 1) / bins <= kMaxPersistList;
 }
 
 template <class V>
 hipError_t launch_persistent(const PrefillArgs& a, hipStream_t stream) {
-  hipLaunchKernelGGL(gdn_prefill_persistent_kernel<V>, dim3(unsigned(device_cus())), dim3(V::NTHREADS), 0, stream, a);
+  if (a.N <= kMaxPersistLpt) {
+    hipLaunchKernelGGL((gdn_prefill_persistent_kernel<V, true>), dim3(unsigned(device_cus())), dim3(V::NTHREADS), 0,
+                       stream, a);
+  } else {
+    hipLaunchKernelGGL((gdn_prefill_persistent_kernel<V, false>), dim3(unsigned(device_cus())), dim3(V::NTHREADS), 0,
+                       stream, a);
+  }
   return hipGetLastError();
 }
 

@@ -504,15 +504,24 @@ PERSISTENT_BATCHES = {
     # empty chain after a non-empty one in another bin's list
     "empty_chains": ([300, 250, 200, 150, 100, 70, 65, 0, 0, 0, 0, 0], Heads(16, 16, 32), True, False,
                      torch.int32),
+    # more than 64 sequences: lists in boustrophedon order over the longest-first
+    # ranks; 200 sequences of 0-200 tokens, 32 v-heads (8 bins, 25 chains each)
+    "hv32_200_seqs": ([int(x) for x in np.random.default_rng(78).integers(0, 201, 200)], Heads(16, 16, 32),
+                      True, False, torch.int32),
+    # 130 sequences of 0-300 tokens, 16 v-heads (16 bins, 8-9 chains each), in place
+    "hv16_130_seqs": ([int(x) for x in np.random.default_rng(79).integers(0, 301, 130)], Heads(8, 8, 16),
+                      True, True, torch.int64),
 }
 
 
 @pytest.mark.parametrize("case", list(PERSISTENT_BATCHES))
 def test_prefill_persistent_batches(gpu, case):
-    """Batches of more (sequence, v-head) chains than CUs (at most 64 sequences, Hv
-    dividing the CU count) run one workgroup per CU, each through a list of chains.
-    Every output and final state against the oracle; three sequences run alone (a
-    split launch) give the packed results bit for bit."""
+    """Batches of more (sequence, v-head) chains than CUs (at most 1,024 sequences, Hv
+    dividing the CU count) run one workgroup per CU, each through a list of chains:
+    a longest-processing-time schedule up to 64 sequences, boustrophedon order over
+    the longest-first ranks beyond.  Every output and final state against the
+    oracle; three sequences run alone (a split launch) give the packed results bit
+    for bit."""
     lens, heads, with_state, in_place, cu_dtype = PERSISTENT_BATCHES[case]
     say(f"prefill persistent batch {case}: {len(lens)} sequences, heads {heads}")
     p = workloads.prefill_inputs(lens, heads, seed=len(lens), gate="slow", state_scale=0.5,
