@@ -511,6 +511,9 @@ PERSISTENT_BATCHES = {
     # 130 sequences of 0-300 tokens, 16 v-heads (16 bins, 8-9 chains each), in place
     "hv16_130_seqs": ([int(x) for x in np.random.default_rng(79).integers(0, 301, 130)], Heads(8, 8, 16),
                       True, True, torch.int64),
+    # 80 sequences of 0-150 tokens, 4 v-heads (64 bins of 4 workgroups, 1-2 chains each)
+    "hv4_80_seqs": ([int(x) for x in np.random.default_rng(80).integers(0, 151, 80)], Heads(2, 2, 4),
+                    True, False, torch.int32),
 }
 
 
