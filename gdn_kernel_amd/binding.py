@@ -219,7 +219,9 @@ def prefill_kernel(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, scale, outp
     accepted); v [T,Hv,128] bf16; state [N,Hv,128,128] fp32 or None; a,b [T,Hv] bf16;
     cu_seqlens [N+1] int32 or int64 on the device; output [T,Hv,128] bf16; new_state
     [N,Hv,128,128] fp32 (may be ``state``).  Calls gdn_prefill, as the TVM-FFI shim
-    does: nothing is allocated, and calls on any streams are independent."""
+    does: nothing is allocated, and calls on any streams give correct results (one long
+    sequence runs two kernels in a scratch of the library, whose launches the library
+    orders on the device)."""
     dev, args = _prefill_args(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, output, new_state)
     args[12] = _scale(scale)
     lib = _lib.load()

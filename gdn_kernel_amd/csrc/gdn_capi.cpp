@@ -37,6 +37,8 @@ static_assert(int64_t(64 + 16) * GDN_MAX_HEADS * 128 < (int64_t(1) << 31),
               "per-chunk row offsets of GDN_MAX_HEADS heads fit 32 bits");
 static_assert(GDN_PREFILL_NO_ALLOC_SCRATCH_BYTES == gdn::kPrefillScratchBytes,
               "the header's scratch size must match the library's");
+static_assert(GDN_PREFILL_DROPIN_SCRATCH_BYTES == gdn::kPrefillDropinScratchBytes,
+              "the header's drop-in scratch size must match the library's");
 
 int check_heads(int32_t hq, int32_t hk, int32_t hv, int32_t dk, int32_t dv) {
   if (hq <= 0 || hk <= 0 || hv <= 0)
@@ -240,7 +242,8 @@ int prefill_impl(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v, const 
                  int32_t cu_seqlens_dtype, int64_t num_seqs, int64_t total_tokens, double scale, gdn_bf16* output,
                  float* new_state, int32_t num_q_heads, int32_t num_k_heads, int32_t num_v_heads,
                  int32_t head_dim_k, int32_t head_dim_v, int32_t spin_limit, int32_t ready_chunks,
-                 uint32_t* aborts, void* workspace, int64_t workspace_bytes, void* stream) {
+                 uint32_t* aborts, void* workspace, int64_t workspace_bytes, void* stream,
+                 bool dropin = false) {
   GDN_TRY(gdn_prefill_check(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu_seqlens_dtype, num_seqs,
                             total_tokens, scale, output, new_state, num_q_heads, num_k_heads, num_v_heads,
                             head_dim_k, head_dim_v));
@@ -270,7 +273,9 @@ int prefill_impl(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v, const 
   args.scale = resolve_scale(scale);
   args.T = total_tokens;
   args.N = int(num_seqs); args.Hq = num_q_heads; args.Hk = num_k_heads; args.Hv = num_v_heads;
-  return device_status(gdn::launch_prefill(args, static_cast<hipStream_t>(stream)), "gdn_prefill launch");
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  return device_status(dropin ? gdn::launch_prefill_dropin(args, st) : gdn::launch_prefill(args, st),
+                       "gdn_prefill launch");
 }
 
 int check_variant(int32_t variant) {
@@ -307,7 +312,7 @@ int gdn_prefill(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v, const f
                 int32_t head_dim_k, int32_t head_dim_v, void* stream) {
   return prefill_impl(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu_seqlens_dtype, num_seqs, total_tokens,
                       scale, output, new_state, num_q_heads, num_k_heads, num_v_heads, head_dim_k, head_dim_v, 0, 0,
-                      nullptr, nullptr, 0, stream);
+                      nullptr, nullptr, 0, stream, true);
 }
 
 int64_t gdn_prefill_workspace_size(int64_t num_seqs, int64_t total_tokens, int32_t num_v_heads) {

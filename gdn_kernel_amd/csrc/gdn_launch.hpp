@@ -70,12 +70,21 @@ int64_t decode_items_per_head(int variant);
 // chains on the current device (the grid times the workgroup size of the variant
 // the launcher picks).
 int64_t prefill_work_items(int64_t chains);
-hipError_t launch_prefill(const PrefillArgs& args, hipStream_t stream);
+// `done`, if not null, is recorded when the launch's last kernel completes (the
+// two-kernel path only: callers that pass it have set args.tiles).
+hipError_t launch_prefill(const PrefillArgs& args, hipStream_t stream, hipEvent_t done = nullptr);
 
 // Bytes of the per-device scratch array of gdn_prefill_no_alloc, and its address
 // on the current device (looked up on the first call per device).
 constexpr int64_t kPrefillScratchBytes = int64_t(64) << 20;
 hipError_t prefill_scratch(void** ptr);
+
+// The drop-in gdn_prefill's launcher: launch_prefill, except that one sequence of at
+// least kDropinTwoKernelTokens tokens runs the two-kernel path in a per-device scratch
+// of the library (kPrefillDropinScratchBytes), ordered between launches by an event.
+constexpr int64_t kPrefillDropinScratchBytes = int64_t(64) << 20;
+constexpr int64_t kDropinTwoKernelTokens = 2048;
+hipError_t launch_prefill_dropin(const PrefillArgs& args, hipStream_t stream);
 
 // Waves of prefill launches on the current device whose hand-off wait gave up,
 // since the library was loaded or the last reset; synchronises the device first.

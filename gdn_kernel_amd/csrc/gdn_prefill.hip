@@ -62,7 +62,10 @@
 // leaving registers.  LDS tiles keep their contraction columns in that order
 // (perm32) so an operand row is one 16-byte read; an operand column of a
 // row-major tile is two ds_read_b64_tr_b16 (transpose reads within 16 lanes).
+#include <hip/hip_ext.h>
+
 #include <atomic>
+#include <mutex>
 #include <type_traits>
 
 #include "gdn_common.hpp"
@@ -2166,11 +2169,18 @@ __global__ __launch_bounds__(PrepVariant::NTHREADS) void gdn_prefill_prep_kernel
   producer_loop<PrepVariant>(sm, p, cs, ce, nchunks, h, hq, hk, 0, wave, lane0, images);
 }
 
+// `done`, if not null, is recorded by the launch itself when the kernel completes
+// (the kernel's own completion signal; no separate marker in the stream).
 template <class V>
-hipError_t launch_variant(const PrefillArgs& a, hipStream_t stream) {
+hipError_t launch_variant(const PrefillArgs& a, hipStream_t stream, hipEvent_t done = nullptr) {
   const int64_t chains = int64_t(a.N) * a.Hv;
   const int64_t grid = V::F == 1 ? (chains + 15) / 16 * 16 : (chains + 7) / 8 * 8 * V::F;
-  hipLaunchKernelGGL(gdn_prefill_kernel<V>, dim3(unsigned(grid)), dim3(V::NTHREADS), 0, stream, a);
+  if (done != nullptr) {
+    hipExtLaunchKernelGGL(gdn_prefill_kernel<V>, dim3(unsigned(grid)), dim3(V::NTHREADS), 0, stream, nullptr, done, 0,
+                          a);
+  } else {
+    hipLaunchKernelGGL(gdn_prefill_kernel<V>, dim3(unsigned(grid)), dim3(V::NTHREADS), 0, stream, a);
+  }
   return hipGetLastError();
 }
 
@@ -2241,6 +2251,65 @@ hipError_t prefill_scratch(void** ptr) {
   return hipSuccess;
 }
 
+// Scratch of the drop-in gdn_prefill's two-kernel path (one long sequence, below):
+// its own array, so that no call of gdn_prefill_no_alloc, captured or not, shares it.
+static __device__ __align__(256) uint8_t dropin_scratch[kPrefillDropinScratchBytes];
+
+namespace {
+
+// Per device: the event that follows the last drop-in launch using dropin_scratch,
+// and the lock that orders the check-launch-record sequence between host threads.
+struct DropinScratch {
+  std::mutex lock;
+  void* addr = nullptr;
+  hipEvent_t done = nullptr;
+  bool used = false;
+};
+DropinScratch g_dropin[kMaxDevices];
+
+}  // namespace
+
+// The drop-in gdn_prefill.  One sequence of at least kDropinTwoKernelTokens tokens,
+// whose chains the launcher splits 4 or 8 ways, runs on the two-kernel path (each
+// chunk prepared once) in dropin_scratch when its images fit; everything else, and
+// any launch on a stream that is being captured into a graph, runs launch_prefill as
+// is.  Launches on the scratch are ordered on the device: each waits (on its stream)
+// for the event recorded after the previous one, so calls on any streams stay
+// correct, and calls on one stream wait for nothing they would not wait for anyway.
+hipError_t launch_prefill_dropin(const PrefillArgs& a, hipStream_t stream) {
+  const int64_t need = a.N == 1 && a.T >= kDropinTwoKernelTokens ? prefill_workspace_bytes(a.N, a.T, a.Hv) : 0;
+  if (need <= 0 || need > kPrefillDropinScratchBytes || a.spin_limit != 0 || a.ready_chunks != 0 ||
+      a.aborts != nullptr || a.tiles != nullptr)
+    return launch_prefill(a, stream);
+  hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+  hipError_t e = hipStreamIsCapturing(stream, &capture);
+  if (e != hipSuccess) return e;
+  if (capture != hipStreamCaptureStatusNone) return launch_prefill(a, stream);
+  int dev = 0;
+  e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  DropinScratch& d = g_dropin[dev];
+  std::lock_guard<std::mutex> guard(d.lock);
+  if (d.addr == nullptr) {
+    e = hipGetSymbolAddress(&d.addr, HIP_SYMBOL(dropin_scratch));
+    if (e != hipSuccess) return e;
+  }
+  if (d.done == nullptr) {
+    e = hipEventCreate(&d.done);
+    if (e != hipSuccess) return e;
+  }
+  if (d.used) {
+    e = hipStreamWaitEvent(stream, d.done, 0);
+    if (e != hipSuccess) return e;
+  }
+  PrefillArgs b = a;
+  b.tiles = static_cast<uint16_t*>(d.addr);
+  e = launch_prefill(b, stream, d.done);  // the state pass records `done` as it completes
+  if (e == hipSuccess) d.used = true;
+  return e;
+}
+
 // Reads (and with `reset` clears) this device's give-up count, after
 // synchronising the device so that every launch so far has finished.
 hipError_t prefill_giveups(uint64_t* count, bool reset) {
@@ -2304,7 +2373,7 @@ int64_t prefill_workspace_bytes(int N, int64_t T, int Hv) {
   return bytes <= kMaxWorkspaceBytes ? bytes : 0;
 }
 
-hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream) {
+hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream, hipEvent_t done) {
   const int F = split_factor(int64_t(a.N) * a.Hv);
   // Launches that use the testing hooks get kernels with the hooks compiled in;
   // production launches keep them out of the device code.
@@ -2330,8 +2399,8 @@ hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream) {
     hipLaunchKernelGGL(gdn_prefill_prep_kernel, dim3(unsigned(grid)), dim3(PrepVariant::NTHREADS), 0, stream, b);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
-    if (F == 4) return launch_variant<Variant<2, 1, false, true>>(a, stream);
-    return launch_variant<Variant<1, 1, false, true>>(a, stream);
+    if (F == 4) return launch_variant<Variant<2, 1, false, true>>(a, stream, done);
+    return launch_variant<Variant<1, 1, false, true>>(a, stream, done);
   }
   // Split chains use 16-row consumer waves (VT = 1), whose per-chunk chain is
   // shorter than a 32-row wave's.  Unsplit chains (F = 1) keep four 32-row waves:

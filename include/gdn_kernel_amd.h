@@ -123,7 +123,18 @@ int gdn_decode_pooled_check(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16
  *             so malformed offsets cannot make the kernel read out of bounds.
  *   output    [T,Hv,128] bf16
  *   new_state [N,Hv,128,128] fp32 final states; may alias state.
+ * Nothing is allocated per call.  One sequence (num_seqs == 1) of at least 2,048
+ * tokens, whose chains the launcher splits over several workgroups, runs the
+ * two-kernel path of gdn_prefill_with_workspace (each chunk prepared once) in a
+ * scratch array the library holds on each device (GDN_PREFILL_DROPIN_SCRATCH_BYTES,
+ * its own, not gdn_prefill_no_alloc's), when its chunk images fit; the results are
+ * the same bit for bit.  The library orders those launches on the device (each
+ * waits, on its stream, for an event that the previous one records as it
+ * completes), so calls on any streams stay correct; on a stream that is being
+ * captured into a graph such a call runs one kernel instead.
  */
+#define GDN_PREFILL_DROPIN_SCRATCH_BYTES (64LL << 20)
+
 int gdn_prefill(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v,
                 const float* state, const float* A_log, const gdn_bf16* a,
                 const float* dt_bias, const gdn_bf16* b, const void* cu_seqlens,
@@ -143,7 +154,7 @@ int gdn_prefill_check(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v,
 /*
  * Prefill with a caller-owned device workspace.  No reference counterpart (the
  * reference allocates nothing and has no workspace argument); the Python
- * `kernel` binding uses it.  Batches of few (sequence, head) chains (at most 64
+ * binding's `prefill_kernel_with_workspace` calls it.  Batches of few (sequence, head) chains (at most 64
  * on a 256-CU device) are split 4 or 8 ways across workgroups, each of which
  * would repeat the chunk preparation (T~ and P).  With a workspace, the
  * preparation runs once per chunk in a first kernel, for all chunks in

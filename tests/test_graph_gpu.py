@@ -49,12 +49,13 @@ def test_decode_graph_replays_match_eager(gpu):
 
 
 @pytest.mark.parametrize("path", ["drop-in", "workspace", "no-alloc"])
-@pytest.mark.parametrize("lens", [[130, 3, 0, 64], [300]])
+@pytest.mark.parametrize("lens", [[130, 3, 0, 64], [300], [2500]])
 def test_prefill_graph_replays_match_eager(gpu, lens, path):
     """128 chains (one kernel) and 32 chains (split 8 ways), through the drop-in kernel
     (gdn_prefill), with a preallocated workspace (two kernels for 32 chains), and through
     gdn_prefill_no_alloc (two kernels in the library's scratch, nothing allocated during
-    capture)."""
+    capture).  One 2,500-token sequence through the drop-in runs two kernels in the
+    drop-in scratch when eager and one kernel when captured; both give the same bits."""
     say(f"prefill graph replay lens={lens} path={path}")
     p = workloads.prefill_inputs(lens, seed=32, device=gpu, gate="slow", state_scale=0.5)
     T, N = p["q"].shape[0], len(p["lengths"])

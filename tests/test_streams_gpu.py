@@ -18,18 +18,25 @@ def _outputs(p, N):
 
 
 def test_concurrent_streams_match_sequential(gpu):
-    """Four streams: decode B=64 out of place; prefill with 128 chains (split 2 ways);
+    """Six streams: decode B=64 out of place; prefill with 128 chains (split 2 ways);
     prefill with 32 chains (split 8 ways); the same 32 chains with a workspace (prep
-    kernel + state pass).  Each stream launches its call three times
-    with no synchronisation in between."""
-    say("concurrent streams: decode B=64, prefill 128 chains, 32 chains, 32 chains with a workspace")
+    kernel + state pass); and two drop-in calls on one 3,000-token sequence, which run
+    the two-kernel path in the library's drop-in scratch (ordered between the streams by
+    the library).  Each stream launches its call three times with no synchronisation in
+    between."""
+    say("concurrent streams: decode B=64, prefill 128 chains, 32 chains, 32 chains with a workspace, "
+        "two 3,000-token drop-in calls")
     w = workloads.decode_inputs(64, seed=51, device=gpu, gate="slow", state_scale=0.5)
     pa = workloads.prefill_inputs([700, 64, 5, 300], seed=52, device=gpu, gate="slow", state_scale=0.5)
     pb = workloads.prefill_inputs([1500], seed=53, device=gpu, gate="slow", state_scale=0.5)
+    pc = workloads.prefill_inputs([3000], seed=54, device=gpu, gate="slow", state_scale=0.5)
+    pd = workloads.prefill_inputs([3000], seed=55, device=gpu, gate="slow", state_scale=0.5)
     dec_o, dec_s = torch.empty_like(w["v"]), torch.empty_like(w["state"])
     a_o, a_s = _outputs(pa, 4)
     b_o, b_s = _outputs(pb, 1)
     c_o, c_s = _outputs(pb, 1)
+    e_o, e_s = _outputs(pc, 1)
+    f_o, f_s = _outputs(pd, 1)
     T, Hv = pb["v"].shape[0], pb["v"].shape[1]
     nbytes = binding.prefill_workspace_bytes(1, T, Hv)
     assert nbytes > 0, "the 32-chain batch is expected to take the two-kernel path"
@@ -45,8 +52,10 @@ def test_concurrent_streams_match_sequential(gpu):
         lambda: binding.prefill_kernel(*pre(pa, a_o, a_s)),
         lambda: binding.prefill_kernel(*pre(pb, b_o, b_s)),
         lambda: binding.prefill_kernel_with_workspace(*pre(pb, c_o, c_s), ws),
+        lambda: binding.prefill_kernel(*pre(pc, e_o, e_s)),
+        lambda: binding.prefill_kernel(*pre(pd, f_o, f_s)),
     ]
-    results = [(dec_o, dec_s), (a_o, a_s), (b_o, b_s), (c_o, c_s)]
+    results = [(dec_o, dec_s), (a_o, a_s), (b_o, b_s), (c_o, c_s), (e_o, e_s), (f_o, f_s)]
 
     for call in calls:                          # one after another on the current stream
         call()
