@@ -1926,10 +1926,11 @@ __device__ __forceinline__ uint32_t wave_min(uint32_t x) {
 // one (a workgroup per chain pays for that, its start-up and its drain once per
 // chain: about three chunk times).  The grid is B = gridDim.x / Hv bins of Hv
 // workgroups; workgroup (bin, i) runs v-head h(i) of every sequence of its bin.
-// Every workgroup forms the same longest-processing-time schedule of the
-// sequences over the bins (longest first, each onto the least-loaded bin; cost 3
-// per chunk + 2 per sequence, ties to the lower bin), so all heads of a sequence
-// share one bin and a bin's workgroups share their list.
+// Every workgroup forms the same schedule of the sequences over the bins, so all
+// heads of a sequence share one bin and a bin's workgroups share their list: with
+// LPT (at most kMaxPersistLpt sequences) longest-processing-time (longest first,
+// each onto the least-loaded bin; cost 3 per chunk + 2 per sequence, ties to the
+// lower bin), otherwise boustrophedon rounds over the longest-first order.
 template <class V, bool LPT>
 __global__ __launch_bounds__(V::NTHREADS) void gdn_prefill_persistent_kernel(PrefillArgs p) {
   static_assert(V::kPersist && V::NCW == 4 && V::VT == 2, "persistent kernel: Variant<4, 2, ..., true>");
