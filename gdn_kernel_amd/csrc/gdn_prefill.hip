@@ -2260,6 +2260,8 @@ namespace {
 
 // Per device: the event that follows the last drop-in launch using dropin_scratch,
 // and the lock that orders the check-launch-record sequence between host threads.
+// The address and the event are created on first use and kept until the process
+// ends, like the scratch itself.
 struct DropinScratch {
   std::mutex lock;
   void* addr = nullptr;
