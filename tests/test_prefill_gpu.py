@@ -577,3 +577,26 @@ def test_prefill_persistent_bounded_waits(gpu):
     torch.cuda.synchronize()
     assert torch.equal(o3, o1) and torch.equal(s3, s1)
     assert binding.prefill_giveups() == 0
+
+
+@pytest.mark.parametrize("in_place", [False, True])
+def test_prefill_dropin_scratch_path(gpu, in_place):
+    """One sequence of at least 2,048 tokens through the drop-in runs two kernels in the
+    library's drop-in scratch: a 2,500-token sequence with an initial state (updated in
+    place or not) and int64 offsets against the oracle, twice in a row (the second call
+    waits for the first one's use of the scratch), and bit for bit equal to
+    gdn_prefill_with_workspace."""
+    say(f"prefill drop-in scratch path, 2,500 tokens, in_place={in_place}")
+    p = workloads.prefill_inputs([2500], seed=61, gate="slow", state_scale=0.5, cu_dtype=torch.int64)
+    o_ref, s_ref = oracle_prefill(p)
+    out, ns = run_prefill(p, gpu, in_place=in_place)
+    out2, ns2 = run_prefill(p, gpu, in_place=False)
+    torch.cuda.synchronize()
+    assert_close(host(out), o_ref, OUT_RTOL, OUT_ATOL, "output")
+    assert_close(host(ns), s_ref, STATE_RTOL, STATE_ATOL, "new_state")
+    assert torch.equal(out2, out)
+    if not in_place:
+        assert torch.equal(ns2, ns)
+    o3, s3 = _prefill_capi(p, gpu, workspace=True)
+    torch.cuda.synchronize()
+    assert torch.equal(o3, out) and (in_place or torch.equal(s3, ns))
