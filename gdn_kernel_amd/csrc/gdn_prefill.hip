@@ -925,11 +925,17 @@ __device__ __forceinline__ void copy_tiles_out(const ChunkBufs& cb, u32x4* image
   }
 }
 
-// Persistent kernel: the first chain at or after position k of the workgroup's
-// list that has tokens (sm.pcount if none).
+// Persistent kernel: the number of chains in the workgroup's list, and the first
+// chain at or after position k that has tokens (chain_count if none).
+template <class Smem>
+__device__ __forceinline__ int chain_count(Smem& sm) {
+  return min(sm.pcount, kMaxPersistList);
+}
+
 template <class Smem>
 __device__ __forceinline__ int next_chain(Smem& sm, int k) {
-  while (k < sm.pcount && sm.ps1[k] <= sm.ps0[k]) ++k;
+  const int n = chain_count(sm);
+  while (k < n && sm.ps1[k] <= sm.ps0[k]) ++k;
   return k;
 }
 
@@ -1004,7 +1010,7 @@ __device__ __forceinline__ void producer_loop(Smem& sm, const PrefillArgs& p, in
           listed = true;
         }
         const int nk = next_chain(sm, k + 1);
-        if (nk < sm.pcount) {
+        if (nk < chain_count(sm)) {
           has_next = true;
           ncs = sm.ps0[nk];
           nclen = int(sm.ps1[nk] - ncs < C ? sm.ps1[nk] - ncs : C);
@@ -1140,7 +1146,7 @@ __device__ __forceinline__ void producer_loop(Smem& sm, const PrefillArgs& p, in
     break;
   } else {
     k = next_chain(sm, k + 1);
-    if (k >= sm.pcount) break;
+    if (k >= chain_count(sm)) break;
     s0 = sm.ps0[k];
     s1 = sm.ps1[k];
     nchunks = int((s1 - s0 + C - 1) / C);
@@ -1984,6 +1990,14 @@ __global__ __launch_bounds__(V::NTHREADS) void gdn_prefill_persistent_kernel(Pre
       sm.spin_limit = p.spin_limit > 0 ? p.spin_limit : kSpinLimit;
       sm.aborts = p.aborts;
     }
+    // Every list entry starts as an empty chain, so that no path (a wait for the list
+    // that gave up included) reads one that was never written.
+    for (int e = tid; e < kMaxPersistList; e += NTHREADS) {
+      sm.pseq[e] = 0;
+      sm.ps0[e] = 0;
+      sm.ps1[e] = 0;
+    }
+    if (tid == 0) sm.pcount = 1;
   }
   __syncthreads();
   for (int s = tid; s < p.N; s += NTHREADS) {
@@ -2094,7 +2108,7 @@ __global__ __launch_bounds__(V::NTHREADS) void gdn_prefill_persistent_kernel(Pre
     }
     if (k == 0) {
       wait_count<V::kHooks>(sm, kList, 1);  // the rest of the list
-      nchains = sm.pcount;
+      nchains = chain_count(sm);
     }
   }
   if (aborted(sm)) {
