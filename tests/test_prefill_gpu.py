@@ -514,6 +514,10 @@ PERSISTENT_BATCHES = {
     # 80 sequences of 0-150 tokens, 4 v-heads (64 bins of 4 workgroups, 1-2 chains each)
     "hv4_80_seqs": ([int(x) for x in np.random.default_rng(80).integers(0, 151, 80)], Heads(2, 2, 4),
                     True, False, torch.int32),
+    # distinct q and k head ratios (v-head h reads q-head h / 4 and k-head h / 2):
+    # 20 sequences of 0-300 tokens, 32 v-heads
+    "hq8_hk16_hv32": ([int(x) for x in np.random.default_rng(81).integers(0, 301, 20)], Heads(8, 16, 32),
+                      True, False, torch.int32),
 }
 
 
