@@ -88,7 +88,8 @@ constexpr int TSTR = 72;     // bf16 row stride of 64-wide tiles (T~, P, N)
 constexpr int NDB = 16 * 16 + 4;  // floats per diagonal N block (column-major; padded by 16 bytes)
 constexpr int NROWS = C - 16;  // rows of N kept for the off-diagonal solve
 
-template <int NCW_, int VT_, bool HOOKS_ = false, bool LOAD_ = false, int NP_ = 4, bool PERSIST_ = false>
+template <int NCW_, int VT_, bool HOOKS_ = false, bool LOAD_ = false, int NP_ = 4, bool PERSIST_ = false,
+          bool TSPLIT_ = false>
 struct Variant {
   static constexpr bool kHooks = HOOKS_;         // testing hooks of PrefillArgs compiled in
   static constexpr bool kLoad = LOAD_;           // waves NCW.. load prepared T~/P (two-kernel path)
@@ -97,7 +98,10 @@ struct Variant {
   static constexpr int NP = NP_;                 // producer (or loader) waves: 4; or 7 (6) beside one (two) consumers
   static constexpr int VT = VT_;                 // 16-row state tiles per consumer wave
   static constexpr int VW = 16 * VT;             // state rows per consumer wave
-  static constexpr int ROWS = NCW * VW;          // state rows per workgroup
+  // Token-split state pass (consumer_loop_tsplit): the consumer waves hold the same
+  // 16 state rows and share each chunk's tokens.
+  static constexpr bool kTokenSplit = TSPLIT_;
+  static constexpr int ROWS = TSPLIT_ ? VW : NCW * VW;  // state rows per workgroup
   static constexpr int F = 128 / ROWS;           // workgroups per chain
   static constexpr int NTHREADS = 64 * (NCW + NP);
   static constexpr int VSEG = 8 * ROWS;          // 16-byte segments of the V slice of a chunk
@@ -112,6 +116,7 @@ struct Variant {
   // (gdn_prefill_persistent_kernel); the four-producer F = 1 layout only.
   static constexpr bool kPersist = PERSIST_;
   static_assert(!PERSIST_ || (NCW_ == 4 && VT_ == 2 && NP_ == 4 && !LOAD_), "persistent: F = 1 only");
+  static_assert(!TSPLIT_ || (NCW_ == 4 && VT_ == 1 && NP_ == 4 && LOAD_ && !PERSIST_), "token split: state pass, F = 8");
 };
 
 // Production launch variants by split factor F (workgroups per chain).  With F = 8
@@ -133,17 +138,21 @@ using PersistVariant = Variant<4, 2, HOOKS, false, 4, true>;
 // The prep kernel of the two-kernel path: the four producer waves alone (no
 // consumers, no V staging); they copy each chunk's tiles out themselves (kCopy).
 struct PrepVariant {
-  static constexpr bool kHooks = false, kLoad = false, kCopy = true, kPipelined = false, kPersist = false;
+  static constexpr bool kHooks = false, kLoad = false, kCopy = true, kPipelined = false, kPersist = false,
+                        kTokenSplit = false;
   static constexpr int NCW = 0, NP = 4, VT = 1, VW = 16, ROWS = 128, F = 1;
   static constexpr int NTHREADS = 64 * (NCW + 4);
   static constexpr int VSEG = 0;
 };
 
 // Prepared tiles of one chunk-head in the workspace: the LDS images of T~ hi,
-// T~ lo and P, in that order (strictly-upper blocks zero), in 16-byte units.
-// Chunk t of sequence s, v-head h is image (s TC + t) Hv + h, TC = ceil(T / C)
-// (a sequence clamped into [0, T] has at most TC chunks).
-constexpr int kTileImage = 3 * C * TSTR / 8;
+// T~ lo and P, in that order (strictly-upper blocks zero), then the chunk's gates
+// beta_c, e^{gamma_c} and e^{gamma_last - gamma_c} (fp32, 64 each), in 16-byte
+// units.  Chunk t of sequence s, v-head h is image (s TC + t) Hv + h, TC = ceil(T /
+// C) (a sequence clamped into [0, T] has at most TC chunks).
+constexpr int kTileUnits = 3 * C * TSTR / 8;
+constexpr int kGateUnits = 3 * C / 4;
+constexpr int kTileImage = kTileUnits + kGateUnits;
 constexpr int kMaxSortedSeqs = 1024;  // longest-first ordering up to this many sequences
 constexpr int kMaxPersistList = 128;  // chains per workgroup of the persistent kernel
 constexpr int kMaxPersistLpt = 64;    // batches of at most this many sequences get a longest-processing-time list
@@ -177,6 +186,15 @@ struct __align__(16) PrefillSmem {
   unsigned* aborts;           // kernels with testing hooks: optional count of waits that gave up
 };
 
+// The token-split state pass exchanges Y and the state's bf16 hi/lo parts through
+// Nh/Nl (unused without producers): four 16-token blocks of Y and four 32-column
+// blocks of the state, 16 and 32 bytes per lane.
+constexpr int kYxBytes = 4 * 64 * 16 + 4 * 64 * 32;
+static_assert(offsetof(PrefillSmem, Nh) % 16 == 0 &&
+                  offsetof(PrefillSmem, Nl) == offsetof(PrefillSmem, Nh) + sizeof(PrefillSmem::Nh) &&
+                  sizeof(PrefillSmem::Nh) + sizeof(PrefillSmem::Nl) >= kYxBytes,
+              "Y exchange fits Nh and Nl");
+
 // LDS of the prep kernel (two-kernel path): one chunk's buffers (the producers
 // stage chunk t + 1 once the copier has written chunk t out) and no V, so that two
 // workgroups share a CU.
@@ -200,6 +218,16 @@ struct __align__(16) PrepSmem {
   int spin_limit;
   unsigned* aborts;
 };
+
+// Gate arrays are copied to and from chunk images in 16-byte units, addressed from
+// beta (gate_unit): 16-byte aligned, e^gamma and the update decay following it.
+template <class Smem>
+constexpr bool gates_follow_beta() {
+  return offsetof(Smem, bet) % 16 == 0 && offsetof(Smem, eg) == offsetof(Smem, bet) + sizeof(Smem::bet) &&
+         offsetof(Smem, dd) == offsetof(Smem, eg) + sizeof(Smem::eg) &&
+         sizeof(Smem::bet) == Smem::kParities * C * sizeof(float);
+}
+static_assert(gates_follow_beta<PrefillSmem>() && gates_follow_beta<PrepSmem>(), "gate layout");
 
 constexpr float kLog2e = 1.4426950408889634f;
 
@@ -433,7 +461,9 @@ enum SyncCounter {
   kStaged = 7,    // pipelined: the chunk's K/Q staged and its gates stored (NS + 1 a chunk)
   kNRead = 8,     // pipelined: the left off-diagonal wave read its N operands
   kVStaged = 9,   // pipelined: the chunk's V staged (NS a chunk)
-  kList = 10      // persistent kernel: the workgroup's chain list is complete (1)
+  kList = 10,     // persistent kernel: the workgroup's chain list is complete (1)
+  kYx = 11,       // token-split state pass: a consumer wave stored its block of Y (4 a chunk)
+  kSx = 12        // token-split state pass: a consumer wave stored its state columns (4 a chunk, 4 at start)
 };
 constexpr int kSpinLimit = 1 << 21;  // default polls (about 70 ms) before a wait gives up
 
@@ -914,15 +944,27 @@ __device__ __forceinline__ void stage_kq_gates(const ChunkBufs& cb, const Produc
   if (pw == 0) store_gates(cb, chunk_gates(f, lane, clen, neg_decay, dt_bias), lane);
 }
 
+// Unit g of a chunk's gates (beta, e^gamma, e^{gamma_last - gamma}; 16 units each),
+// as an offset from beta, so that the address stays a known LDS address.
+template <class Smem>
+__device__ __forceinline__ float* gate_unit(const ChunkBufs& cb, int g) {
+  return cb.bet + (g >> 4) * (Smem::kParities * C) + 4 * (g & 15);
+}
+
 // Producer thread pt's share of a chunk's T~ hi, T~ lo and P tiles (their LDS
-// images) to the chunk's image in the workspace; NaN images once a hand-off wait
-// of the workgroup gave up.
+// images) and gates to the chunk's image in the workspace; NaN images once a
+// hand-off wait of the workgroup gave up.  The gates go out from the first wave,
+// which stores the next chunk's gates after this copy.
+template <class Smem>
 __device__ __forceinline__ void copy_tiles_out(const ChunkBufs& cb, u32x4* image, int pt, bool poison) {
   constexpr int NT1 = C * TSTR / 8;
-  for (int e = pt; e < kTileImage; e += NPROD) {
+  constexpr u32x4 nan4 = u32x4{kNaNx2, kNaNx2, kNaNx2, kNaNx2};
+  for (int e = pt; e < kTileUnits; e += NPROD) {
     const uint16_t* src = e < NT1 ? cb.Th + 8 * e : e < 2 * NT1 ? cb.Tl + 8 * (e - NT1) : cb.P + 8 * (e - 2 * NT1);
-    image[e] = poison ? u32x4{kNaNx2, kNaNx2, kNaNx2, kNaNx2} : *reinterpret_cast<const u32x4*>(src);
+    image[e] = poison ? nan4 : *reinterpret_cast<const u32x4*>(src);
   }
+  if (pt < kGateUnits)
+    image[kTileUnits + pt] = poison ? nan4 : *reinterpret_cast<const u32x4*>(gate_unit<Smem>(cb, pt));
 }
 
 // Persistent kernel: the number of chains in the workgroup's list, and the first
@@ -1024,7 +1066,7 @@ __device__ __forceinline__ void producer_loop(Smem& sm, const PrefillArgs& p, in
     if constexpr (V::kCopy) {
       if (t >= 1) {
         wait_count<V::kHooks>(sm, kReady, 4 * t);  // chunk t - 1 handed over by all four waves
-        copy_tiles_out(chunk_bufs(sm, (t - 1) & 1), images + int64_t(t - 1) * p.Hv * kTileImage, pt, aborted(sm));
+        copy_tiles_out<Smem>(chunk_bufs(sm, (t - 1) & 1), images + int64_t(t - 1) * p.Hv * kTileImage, pt, aborted(sm));
       }
     }
     clk.lap(0);
@@ -1154,7 +1196,7 @@ __device__ __forceinline__ void producer_loop(Smem& sm, const PrefillArgs& p, in
   }
   if constexpr (V::kCopy) {
     wait_count<V::kHooks>(sm, kReady, 4 * nchunks);
-    copy_tiles_out(chunk_bufs(sm, (nchunks - 1) & 1), images + int64_t(nchunks - 1) * p.Hv * kTileImage, pt,
+    copy_tiles_out<Smem>(chunk_bufs(sm, (nchunks - 1) & 1), images + int64_t(nchunks - 1) * p.Hv * kTileImage, pt,
                    aborted(sm));
   }
   clk.store(V::NCW + pw, lane0);
@@ -1405,8 +1447,6 @@ __device__ __forceinline__ void loader_loop(PrefillSmem& sm, const PrefillArgs& 
   constexpr int NTIT = (kTileImage + NPROD - 1) / NPROD;     // 16-byte tile units per loader thread
   constexpr int NT1 = C * TSTR / 8;                          // 16-byte units per tile
   const int pt = pw * 64 + lane0;
-  const float neg_decay = -expf(p.A_log[h]);
-  const float dt_bias = p.dt_bias[h];
   const LaneOffsets lo = {(pt >> 4) * p.Hk * D + 8 * (pt & 15), (pt >> 4) * p.Hq * D + 8 * (pt & 15), pt * p.Hv};
   int voff[NVIT], vrow[NVIT];
 #pragma unroll
@@ -1449,15 +1489,17 @@ __device__ __forceinline__ void loader_loop(PrefillSmem& sm, const PrefillArgs& 
     const ChunkBufs cb = chunk_bufs(sm, t & 1);
     if (t >= 2) wait_count<V::kHooks>(sm, kConsumed, V::NCW * (t - 1));  // chunk t - 2 consumed
     clk.lap(0);
-    stage_kq_gates(cb, f, pt, pw, lane, clen, neg_decay, dt_bias);
+    stage_kq(cb, f, pt);
     if (ncs < s1) producer_prefetch(p, ncs, nclen, h, hq, hk, pt, lo, f);
     clk.lap(1);
 #pragma unroll
     for (int it = 0; it < NTIT; ++it) {
       const int e = pt + it * NPROD;
-      if (e < kTileImage) {
+      if (e < kTileUnits) {
         uint16_t* dst = e < NT1 ? cb.Th + 8 * e : e < 2 * NT1 ? cb.Tl + 8 * (e - NT1) : cb.P + 8 * (e - 2 * NT1);
         *reinterpret_cast<u32x4*>(dst) = tv[it];
+      } else if (e < kTileImage) {
+        *reinterpret_cast<u32x4*>(gate_unit<PrefillSmem>(cb, e - kTileUnits)) = tv[it];
       }
     }
     clk.lap(7);
@@ -1743,6 +1785,171 @@ __device__ __forceinline__ void consumer_loop(PrefillSmem& sm, const PrefillArgs
   clk.store(wave, lane0);
 }
 
+// The token-split consumer loop of the two-kernel state pass (F = 8).  The four
+// consumer waves share the slice's 16 state rows: wave w keeps state columns
+// 32w .. 32w + 31 in fp32, forms the rows of X = K S^T, Y and the output of the
+// chunk's tokens 16w .. 16w + 15, and updates its own columns.  Two LDS exchanges a
+// chunk give every wave what the others formed: the four blocks of Y (for v_new, which
+// every wave forms whole) and the bf16 hi/lo parts of the four column blocks of the
+// state (for the next retrieve).  Each value is produced by the same operations in the
+// same order as in consumer_loop with one 16-row wave, so the results are
+// bit-identical, while the chain of a chunk loses three quarters of the retrieve, Y,
+// the output and the state update.
+//
+// Each exchange buffer is single: a wave rewrites its block of Y (of the state) only
+// after the wait for all four blocks of the other exchange, which every wave signals
+// after its last read of the previous contents.
+template <class V>
+__device__ __forceinline__ void consumer_loop_tsplit(PrefillSmem& sm, const PrefillArgs& p, int64_t s0, int64_t s1,
+                                                     int nchunks, int h, int row0, int wave, int lane0,
+                                                     f32x4 (&S)[2]) {
+  static_assert(V::kTokenSplit && V::VT == 1 && V::NCW == 4, "token-split consumers");
+  const int64_t vstride = int64_t(p.Hv) * D;
+  const int ct = wave;  // this wave's 16-token block and 32-column block
+  const int orow = (16 * ct + (lane0 & 15)) * int(vstride) + 4 * (lane0 >> 4);
+  f32x4* const yx = reinterpret_cast<f32x4*>(sm.Nh);            // Y: [block][lane]
+  uint4* const sx = reinterpret_cast<uint4*>(sm.Nh) + 4 * 64;   // state: [block][hi, lo][lane]
+  // K^T operand base of column blocks 2 ct, 2 ct + 1 (kt_bases with kt / 2 = ct).
+  int ktb;
+  {
+    const int j = lane0 & 15, rl = 4 * (lane0 >> 4) + (j >> 2), sl = kq_sigma(rl);
+    ktb = rl * KSTR + 8 * ((j & 3) ^ (sl & 3)) + 32 * (ct ^ (sl >> 2));
+  }
+  {
+    uint4 Sh, Sl;
+    split_pack(S[0], S[1], Sh, Sl);
+    sx[(2 * ct) * 64 + lane0] = Sh;
+    sx[(2 * ct + 1) * 64 + lane0] = Sl;
+    signal_count(sm, kSx, lane0);
+  }
+  PhaseClock clk;
+  clk.start();
+  for (int t = 1; t <= nchunks; ++t) {
+    int lane = lane0;
+    asm volatile("" : "+v"(lane));
+    const int g = lane >> 4, n16 = lane & 15;
+    const int64_t cs = s0 + int64_t(t - 1) * C;
+    const int clen = int(s1 - cs < C ? s1 - cs : C);
+    const ChunkBufs cb = chunk_bufs(sm, (t - 1) & 1);
+    wait_count<V::kHooks>(sm, kReady, 4 * t);  // chunk t - 1 loaded
+    uint4 kf[4], qf[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      kf[ks] = frag_kq(cb.K, 16 * ct, ks, lane);
+      qf[ks] = frag_kq(cb.Q, 16 * ct, ks, lane);
+    }
+    wait_count<V::kHooks>(sm, kSx, 4 * t);  // the state after chunk t - 2
+    uint4 Sh[4], Sl[4];
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      Sh[ks] = sx[(2 * ks) * 64 + lane];
+      Sl[ks] = sx[(2 * ks + 1) * 64 + lane];
+    }
+    clk.lap(0);
+
+    // 1: block ct of X = K S^T and of (Q S^T)^T.
+    f32x4 xk = zero4(), xq = zero4();
+#pragma unroll
+    for (int ks = 0; ks < 4; ++ks) {
+      xk = mfma(kf[ks], Sh[ks], xk);
+      xk = mfma(kf[ks], Sl[ks], xk);
+      xq = mfma(Sh[ks], qf[ks], xq);
+    }
+    clk.lap(1);
+
+    // 2: Y for rows c = 16ct + 4g + i, as consumer_loop; the output block scaled.
+    {
+      const float4 bc = *reinterpret_cast<const float4*>(cb.bet + 16 * ct + 4 * g);
+      const float4 ec = *reinterpret_cast<const float4*>(cb.eg + 16 * ct + 4 * g);
+      const float b4[4] = {bc.x, bc.y, bc.z, bc.w}, e4[4] = {ec.x, ec.y, ec.z, ec.w};
+      const uint2 vv = read_tr(sm.V + (16 * ct + 4 * g + (n16 >> 2)) * VSTR + vrow<1>(0, 4 * (n16 & 3)));
+      const float vf[4] = {bf16lo_f32(vv.x), bf16hi_f32(vv.x), bf16lo_f32(vv.y), bf16hi_f32(vv.y)};
+#pragma unroll
+      for (int i = 0; i < 4; ++i) xk[i] = b4[i] * (vf[i] - e4[i] * xk[i]);
+      xq = xq * (cb.eg[16 * ct + n16] * p.scale);
+    }
+    signal_count(sm, kVFree, lane);  // V of this chunk read
+    yx[64 * ct + lane] = xk;
+    signal_count(sm, kYx, lane);
+    // T~ (all of it) and this block's P operands, read while the other blocks arrive.
+    uint4 thf[6], tlf[6];
+#pragma unroll
+    for (int c = 0; c < 4; ++c)
+#pragma unroll
+      for (int js = 0; js <= (c >> 1); ++js) {
+        const int i = c < 2 ? c : 2 * c - 2 + js;
+        thf[i] = frag(cb.Th, TSTR, 16 * c, js, lane);
+        tlf[i] = frag(cb.Tl, TSTR, 16 * c, js, lane);
+      }
+    const uint4 pq0 = frag(cb.P, TSTR, 16 * ct, 0, lane);
+    const uint4 pq1 = frag(cb.P, TSTR, 16 * ct, 1, lane);
+    wait_count<V::kHooks>(sm, kYx, 4 * t);
+    f32x4 Y[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) Y[c] = yx[64 * c + lane];
+    clk.lap(2);
+
+    // v_new = T~ Y, all 64 rows.
+    uint4 Yh[2], Yl[2];
+#pragma unroll
+    for (int js = 0; js < 2; ++js) split_pack(Y[2 * js], Y[2 * js + 1], Yh[js], Yl[js]);
+    f32x4 Vn[4];
+#pragma unroll
+    for (int c = 0; c < 4; ++c) {
+      Vn[c] = zero4();
+#pragma unroll
+      for (int js = 0; js <= (c >> 1); ++js) {
+        const uint4 th = thf[c < 2 ? c : 2 * c - 2 + js], tl = tlf[c < 2 ? c : 2 * c - 2 + js];
+        Vn[c] = mfma(th, Yh[js], Vn[c]);
+        Vn[c] = mfma(th, Yl[js], Vn[c]);
+        Vn[c] = mfma(tl, Yh[js], Vn[c]);
+      }
+    }
+    clk.lap(3);
+
+    // 3: columns 32ct .. 32ct + 31 of S = e^{gamma_last} S + sum_c K[c]^T (d_c v_new[c]).
+    const float dlast = cb.eg[clen - 1];
+    uint4 Uh[2], Ul[2];
+#pragma unroll
+    for (int js = 0; js < 2; ++js) {
+      const float4 d0 = *reinterpret_cast<const float4*>(cb.dd + 32 * js + 4 * g);
+      const float4 d1 = *reinterpret_cast<const float4*>(cb.dd + 32 * js + 16 + 4 * g);
+      const f32x4 e0 = {d0.x, d0.y, d0.z, d0.w}, e1 = {d1.x, d1.y, d1.z, d1.w};
+      split_pack(Vn[2 * js] * e0, Vn[2 * js + 1] * e1, Uh[js], Ul[js]);
+    }
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      S[j] = S[j] * dlast;
+#pragma unroll
+      for (int js = 0; js < 2; ++js) {
+        const uint16_t* kp = cb.K + ktb + 32 * js * KSTR + 4 * j;
+        const uint2 a = read_tr(kp), b = read_tr(kp + 16 * KSTR);
+        const uint4 ak = uint4{a.x, a.y, b.x, b.y};
+        S[j] = mfma(ak, Uh[js], S[j]);
+        S[j] = mfma(ak, Ul[js], S[j]);
+      }
+    }
+    signal_count(sm, kConsumed, lane);  // buffers of this chunk no longer read
+    {
+      uint4 h2, l2;
+      split_pack(S[0], S[1], h2, l2);
+      sx[(2 * ct) * 64 + lane] = h2;
+      sx[(2 * ct + 1) * 64 + lane] = l2;
+      signal_count(sm, kSx, lane);
+    }
+    clk.lap(5);
+
+    // Output block ct: o^T = scale e^gamma (S Q^T) + v_new^T (scale P)^T.
+    xq = mfma(pack_hi(Vn[0], Vn[1]), pq0, xq);
+    if (ct >= 2) xq = mfma(pack_hi(Vn[2], Vn[3]), pq1, xq);
+    if (16 * ct + n16 < clen)
+      *reinterpret_cast<uint2*>(p.out + cs * vstride + (int64_t(h) * D + row0) + orow) =
+          uint2{pack_bf16x2(xq[0], xq[1]), pack_bf16x2(xq[2], xq[3])};
+    clk.lap(4);
+  }
+  clk.store(wave, lane0);
+}
+
 // The sequence of rank `rank` in descending length order (ties: lower index
 // first), so the longest chains start first; natural order for large batches.
 template <int NTHREADS>
@@ -1860,9 +2067,44 @@ __global__ __launch_bounds__(V::NTHREADS) void gdn_prefill_kernel(PrefillArgs p)
     return;
   }
 
-  // Consumer state slab: rows v = row0 + VW*wave + vrow(vt, n16), cols k = 16*kt + 4g + i.
   const int64_t state_head = (int64_t(seq) * p.Hv + h) * D * D;
   const int g = lane0 >> 4, n16 = lane0 & 15;
+  if constexpr (V::kTokenSplit) {
+    // Token-split consumers: wave w holds column blocks 2w and 2w + 1 (cols k = 16 kt +
+    // 4g + i) of the slice's rows v = row0 + n16.
+    const int64_t srow = state_head + int64_t(row0 + n16) * D + 32 * wave + 4 * g;
+    f32x4 S2[2];
+#pragma unroll
+    for (int j = 0; j < 2; ++j) {
+      if (p.state) {
+        const float4 x = *reinterpret_cast<const float4*>(p.state + srow + 16 * j);
+        S2[j] = f32x4{x.x, x.y, x.z, x.w};
+      } else {
+        S2[j] = zero4();
+      }
+    }
+    if (nchunks > 0) {
+      consumer_loop_tsplit<V>(sm, p, s0, s1, nchunks, h, row0, wave, lane0, S2);
+      if (aborted(sm)) {
+        // A hand-off wait gave up: NaN over the slice's outputs (wave w: tokens
+        // s0 + 16 (4m + w) + n16) and state.
+        const int64_t vstride = int64_t(p.Hv) * D;
+        uint16_t* obase = p.out + int64_t(h) * D + row0 + 4 * (lane0 >> 4);
+        for (int64_t tok = s0 + 16 * wave + n16; tok < s1; tok += 64)
+          *reinterpret_cast<uint2*>(obase + tok * vstride) = uint2{kNaNx2, kNaNx2};
+        const float nan = __builtin_nanf("");
+        S2[0] = S2[1] = f32x4{nan, nan, nan, nan};
+      }
+    }
+    if (nchunks > 0 || p.state != p.new_state) {
+#pragma unroll
+      for (int j = 0; j < 2; ++j)
+        *reinterpret_cast<float4*>(p.new_state + srow + 16 * j) = make_float4(S2[j][0], S2[j][1], S2[j][2], S2[j][3]);
+    }
+    return;
+  }
+
+  // Consumer state slab: rows v = row0 + VW*wave + vrow(vt, n16), cols k = 16*kt + 4g + i.
   f32x4 S[VT][8];
 #pragma unroll
   for (int vt = 0; vt < VT; ++vt) {
@@ -2417,7 +2659,7 @@ hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream, hipEvent_t d
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     if (F == 4) return launch_variant<Variant<2, 1, false, true>>(a, stream, done);
-    return launch_variant<Variant<1, 1, false, true>>(a, stream, done);
+    return launch_variant<Variant<4, 1, false, true, 4, false, true>>(a, stream, done);
   }
   // Split chains use 16-row consumer waves (VT = 1), whose per-chunk chain is
   // shorter than a 32-row wave's.  Unsplit chains (F = 1) keep four 32-row waves:

@@ -178,13 +178,15 @@ def test_prefill_fault_injection_rejects(lib, kw, code, frag):
 
 
 def test_prefill_workspace_size(lib):
-    """Bytes of the two-kernel prefill path: N ceil(T / 64) Hv chunk images of 27,648
-    bytes (T~ hi, T~ lo and P, 64 x 72 bf16 each) for batches whose chains are split 4
-    or 8 ways across workgroups (at most 64 chains on 256 CUs), 0 otherwise.  Without
-    a GPU the CU count defaults to 256."""
-    assert lib.gdn_prefill_workspace_size(1, 4096, 32) == 64 * 32 * 27648
-    assert lib.gdn_prefill_workspace_size(3, 100, 8) == 3 * 2 * 8 * 27648
-    assert lib.gdn_prefill_workspace_size(2, 4096, 32) == 2 * 64 * 32 * 27648    # 64 chains
+    """Bytes of the two-kernel prefill path: N ceil(T / 64) Hv chunk images of 28,416
+    bytes (T~ hi, T~ lo and P, 64 x 72 bf16 each, then three 64-float gate vectors) for
+    batches whose chains are split 4 or 8 ways across workgroups (at most 64 chains on
+    256 CUs), 0 otherwise.  Without a GPU the CU count defaults to 256."""
+    image = 3 * 64 * 72 * 2 + 3 * 64 * 4
+    assert image == 28416
+    assert lib.gdn_prefill_workspace_size(1, 4096, 32) == 64 * 32 * image
+    assert lib.gdn_prefill_workspace_size(3, 100, 8) == 3 * 2 * 8 * image
+    assert lib.gdn_prefill_workspace_size(2, 4096, 32) == 2 * 64 * 32 * image    # 64 chains
     assert lib.gdn_prefill_workspace_size(3, 4096, 32) == 0                      # 96 chains: one kernel
     assert lib.gdn_prefill_workspace_size(5, 4096, 32) == 0
     for n, t, hv in ((0, 100, 8), (1, 0, 8), (1, 100, 0), (-1, 100, 8), (1, -5, 8)):
