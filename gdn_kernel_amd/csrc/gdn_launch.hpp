@@ -83,7 +83,7 @@ hipError_t prefill_scratch(void** ptr);
 // least kDropinTwoKernelTokens tokens runs the two-kernel path in a per-device scratch
 // of the library (kPrefillDropinScratchBytes), ordered between launches by an event.
 constexpr int64_t kPrefillDropinScratchBytes = int64_t(64) << 20;
-constexpr int64_t kDropinTwoKernelTokens = 2048;
+constexpr int64_t kDropinTwoKernelTokens = 1024;
 hipError_t launch_prefill_dropin(const PrefillArgs& args, hipStream_t stream);
 
 // Waves of prefill launches on the current device whose hand-off wait gave up,

@@ -123,7 +123,7 @@ int gdn_decode_pooled_check(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16
  *             so malformed offsets cannot make the kernel read out of bounds.
  *   output    [T,Hv,128] bf16
  *   new_state [N,Hv,128,128] fp32 final states; may alias state.
- * Nothing is allocated per call.  One sequence (num_seqs == 1) of at least 2,048
+ * Nothing is allocated per call.  One sequence (num_seqs == 1) of at least 1,024
  * tokens, whose chains the launcher splits over several workgroups, runs the
  * two-kernel path of gdn_prefill_with_workspace (each chunk prepared once) in a
  * scratch array the library holds on each device (GDN_PREFILL_DROPIN_SCRATCH_BYTES,

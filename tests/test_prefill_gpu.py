@@ -585,7 +585,7 @@ def test_prefill_persistent_bounded_waits(gpu):
 
 @pytest.mark.parametrize("in_place", [False, True])
 def test_prefill_dropin_scratch_path(gpu, in_place):
-    """One sequence of at least 2,048 tokens through the drop-in runs two kernels in the
+    """One sequence of at least 1,024 tokens through the drop-in runs two kernels in the
     library's drop-in scratch: a 2,500-token sequence with an initial state (updated in
     place or not) and int64 offsets against the oracle, twice in a row (the second call
     waits for the first one's use of the scratch), and bit for bit equal to

@@ -28,7 +28,7 @@ def test_concurrent_streams_match_sequential(gpu):
         "two 3,000-token drop-in calls")
     w = workloads.decode_inputs(64, seed=51, device=gpu, gate="slow", state_scale=0.5)
     pa = workloads.prefill_inputs([700, 64, 5, 300], seed=52, device=gpu, gate="slow", state_scale=0.5)
-    pb = workloads.prefill_inputs([1500], seed=53, device=gpu, gate="slow", state_scale=0.5)
+    pb = workloads.prefill_inputs([900], seed=53, device=gpu, gate="slow", state_scale=0.5)
     pc = workloads.prefill_inputs([3000], seed=54, device=gpu, gate="slow", state_scale=0.5)
     pd = workloads.prefill_inputs([3000], seed=55, device=gpu, gate="slow", state_scale=0.5)
     dec_o, dec_s = torch.empty_like(w["v"]), torch.empty_like(w["state"])
