@@ -198,7 +198,7 @@ def test_prefill_no_decay_precision_envelope(gpu):
     saturated beta: the state-path operands are bf16 hi + lo pairs (about 16 significant
     bits), so the state error does not decay away and settles at about 5e-6 of the
     head's largest state element.  Near-zero elements of a state whose entries reach ~3
-    can then exceed the strict bound (atol 1e-5 + rtol 1e-3 |ref|) by up to ~15%.  This
+    can then exceed the strict bound (atol 1e-5 + rtol 1e-3 |ref|) by tens of percent.  This
     test pins that envelope: the outputs within the strict tolerance, and every state
     element within 2e-5 x the largest |state| of its head (besides rtol 1e-3)."""
     say("prefill no-decay precision envelope")
