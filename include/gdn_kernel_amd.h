@@ -156,7 +156,7 @@ int gdn_prefill_check(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v,
  * reference allocates nothing and has no workspace argument); the Python
  * binding's `prefill_kernel_with_workspace` calls it.  Batches of few (sequence, head) chains (at most 64
  * on a 256-CU device) are split 4 or 8 ways across workgroups, each of which
- * would repeat the chunk preparation (T~ and P).  With a workspace, the
+ * would repeat the chunk preparation (T~, P and the gates).  With a workspace, the
  * preparation runs once per chunk in a first kernel, for all chunks in
  * parallel, and the state pass only copies it.
  *   gdn_prefill_workspace_size: bytes this path needs for num_seqs sequences,
