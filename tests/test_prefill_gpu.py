@@ -357,13 +357,16 @@ def _prefill_capi(p, gpu, workspace, ws=None, nbytes=None):
     ([130, 2100], Heads(16, 16, 32)),            # 64 chains, split 4 ways
     ([1, 2, 63, 64, 129], Heads(2, 2, 4)),       # boundary lengths (chunk runs of 1 in the prep)
     ([700, 1300], Heads(8, 8, 16)),              # runs of several chunks per prep workgroup
+    ([1000], Heads(16, 8, 32)),                  # distinct q and k head ratios, split 8 ways
 ])
 def test_prefill_two_kernel_path(gpu, lens, heads):
     """Batches of at most 64 chains with a workspace: a first kernel prepares every
-    chunk's T~ and P (all chunks at once) and the state pass copies them instead of
-    recomputing them in each of a chain's 4 or 8 slices.  The preparation is the same code, so the results equal
-    gdn_prefill's bit for bit; both match the oracle.  The workspace starts as 0xFF
-    bytes, so a chunk image that the first kernel did not write would show."""
+    chunk's T~, P and gates (all chunks at once) and the state pass copies them instead
+    of recomputing them in each of a chain's 4 or 8 slices; split 8 ways, four consumer
+    waves share each slice's chunk tokens.  Every value comes from the same operations in
+    the same order, so the results equal gdn_prefill's (here one kernel) bit for bit; both
+    match the oracle.  The workspace starts as 0xFF bytes, so a chunk image that the first
+    kernel did not write would show."""
     say(f"prefill two-kernel path lens={lens} heads={heads}")
     p = workloads.prefill_inputs(lens, heads, seed=22, gate="slow", state_scale=0.5)
     o1, s1 = _prefill_capi(p, gpu, workspace=False)
