@@ -127,13 +127,14 @@ int gdn_decode_pooled_check(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16
  * tokens, whose chains the launcher splits over several workgroups, runs the
  * two-kernel path of gdn_prefill_with_workspace (each chunk prepared once) in a
  * scratch array the library holds on each device (GDN_PREFILL_DROPIN_SCRATCH_BYTES,
- * its own, not gdn_prefill_no_alloc's), when its chunk images fit; the results are
+ * its own, not gdn_prefill_no_alloc's; with 32 v-heads it holds the images of up
+ * to 18,880 tokens), when its chunk images fit; the results are
  * the same bit for bit.  The library orders those launches on the device (each
  * waits, on its stream, for an event that the previous one records as it
  * completes), so calls on any streams stay correct; on a stream that is being
  * captured into a graph such a call runs one kernel instead.
  */
-#define GDN_PREFILL_DROPIN_SCRATCH_BYTES (64LL << 20)
+#define GDN_PREFILL_DROPIN_SCRATCH_BYTES (256LL << 20)
 
 int gdn_prefill(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v,
                 const float* state, const float* A_log, const gdn_bf16* a,

@@ -607,3 +607,21 @@ def test_prefill_dropin_scratch_path(gpu, in_place):
     o3, s3 = _prefill_capi(p, gpu, workspace=True)
     torch.cuda.synchronize()
     assert torch.equal(o3, out) and (in_place or torch.equal(s3, ns))
+
+
+def test_prefill_dropin_long_sequence(gpu):
+    """A 6,000-token sequence (32 v-heads: 85 MB of chunk images, more than 64 MiB) runs
+    two kernels in the drop-in's scratch: against the oracle, and bit for bit equal to
+    gdn_prefill_with_workspace."""
+    say("prefill drop-in, one 6,000-token sequence")
+    lib = _lib.load()
+    p = workloads.prefill_inputs([6000], seed=62, gate="slow", state_scale=0.5)
+    need = lib.gdn_prefill_workspace_size(1, 6000, 32)
+    assert 64 << 20 < need <= _lib.GDN_PREFILL_DROPIN_SCRATCH_BYTES, need
+    o_ref, s_ref = oracle_prefill(p)
+    out, ns = run_prefill(p, gpu)
+    o2, s2 = _prefill_capi(p, gpu, workspace=True)
+    torch.cuda.synchronize()
+    assert_close(host(out), o_ref, OUT_RTOL, OUT_ATOL, "output")
+    assert_close(host(ns), s_ref, STATE_RTOL, STATE_ATOL, "new_state")
+    assert torch.equal(out, o2) and torch.equal(ns, s2)
