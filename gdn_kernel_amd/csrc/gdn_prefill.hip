@@ -89,7 +89,7 @@ constexpr int NDB = 16 * 16 + 4;  // floats per diagonal N block (column-major; 
 constexpr int NROWS = C - 16;  // rows of N kept for the off-diagonal solve
 
 template <int NCW_, int VT_, bool HOOKS_ = false, bool LOAD_ = false, int NP_ = 4, bool PERSIST_ = false,
-          bool TSPLIT_ = false>
+          bool TSPLIT_ = false, bool DEEP_ = false>
 struct Variant {
   static constexpr bool kHooks = HOOKS_;         // testing hooks of PrefillArgs compiled in
   static constexpr bool kLoad = LOAD_;           // waves NCW.. load prepared T~/P (two-kernel path)
@@ -117,6 +117,10 @@ struct Variant {
   static constexpr bool kPersist = PERSIST_;
   static_assert(!PERSIST_ || (NCW_ == 4 && VT_ == 2 && NP_ == 4 && !LOAD_), "persistent: F = 1 only");
   static_assert(!TSPLIT_ || (NCW_ == 4 && VT_ == 1 && NP_ == 4 && LOAD_ && !PERSIST_), "token split: state pass, F = 8");
+  // State pass over images that the caches do not hold (long batches): the loaders
+  // load each chunk's images two chunks ahead instead of one.
+  static constexpr bool kDeepImages = DEEP_;
+  static_assert(!DEEP_ || LOAD_, "image prefetch depth: state pass only");
 };
 
 // Production launch variants by split factor F (workgroups per chain).  With F = 8
@@ -1433,12 +1437,14 @@ __device__ __forceinline__ void producer_loop_split(PrefillSmem& sm, const Prefi
 }
 
 // The loader loop of the two-kernel path: the producers' hand-offs and staging,
-// with chunk t's T~ (hi, lo) and P copied from their prepared images (tiles =
-// image of chunk 0 of this chain; chunk t is Hv images further) instead of
-// computed.  K, Q and the gates are staged as the producers stage them, V at the
-// end of the tick, after the consumers' last read of the previous chunk's V.
+// with chunk t's T~ (hi, lo), P and gates copied from their prepared images (tiles
+// = image of chunk 0 of this chain; chunk t is Hv images further) instead of
+// computed.  K and Q are staged as the producers stage them, V at the end of the
+// tick, after the consumers' last read of the previous chunk's V.
 // The images and V of chunk t + 1 are loaded into registers during tick t, so
-// their latency overlaps the waits for the consumers.
+// their latency overlaps the waits for the consumers; with V::kDeepImages the
+// images of chunk t + 2 (two register sets, alternating), as soon as chunk t's are
+// in LDS.
 template <class V>
 __device__ __forceinline__ void loader_loop(PrefillSmem& sm, const PrefillArgs& p, const u32x4* tiles, int64_t s0,
                                             int64_t s1, int nchunks, int h, int hq, int hk, int row0, int pw,
@@ -1461,12 +1467,20 @@ __device__ __forceinline__ void loader_loop(PrefillSmem& sm, const PrefillArgs& 
 #pragma unroll
   for (int it = 0; it < NTIT; ++it) toff[it] = pt + it * NPROD < kTileImage ? pt + it * NPROD : kTileImage - 1;
   // (First-class vectors: copies of uint4 structs would go through the stack.)
-  u32x4 tv[NTIT], fv[NVIT];
+  constexpr bool deep = V::kDeepImages;
+  u32x4 tva[NTIT], tvb[deep ? NTIT : 1], fv[NVIT];
   ProducerPrefetch f;
   producer_prefetch(p, s0, int(s1 - s0 < C ? s1 - s0 : C), h, hq, hk, pt, lo, f);
-  // Chunk 0's images and V slice into registers.
+  // Chunk 0's images (and chunk 1's) and chunk 0's V slice into registers.
 #pragma unroll
-  for (int it = 0; it < NTIT; ++it) tv[it] = tiles[toff[it]];
+  for (int it = 0; it < NTIT; ++it) tva[it] = tiles[toff[it]];
+  if constexpr (deep) {
+    if (nchunks > 1) {
+      const u32x4* src = tiles + int64_t(p.Hv) * kTileImage;
+#pragma unroll
+      for (int it = 0; it < NTIT; ++it) tvb[it] = src[toff[it]];
+    }
+  }
   {
     const int clen0 = int(s1 - s0 < C ? s1 - s0 : C);
     const uint16_t* vb = p.v + (s0 * p.Hv + h) * D + row0;
@@ -1479,11 +1493,10 @@ __device__ __forceinline__ void loader_loop(PrefillSmem& sm, const PrefillArgs& 
   PhaseClock clk;
   clk.start();
 
-  for (int t = 0; t < nchunks; ++t) {
+  auto tick = [&](int t, u32x4(&tv)[NTIT]) {
     int lane = lane0;
     asm volatile("" : "+v"(lane));
     const int64_t cs = s0 + int64_t(t) * C;
-    const int clen = int(s1 - cs < C ? s1 - cs : C);
     const int64_t ncs = cs + C;
     const int nclen = int(s1 - ncs < C ? s1 - ncs : C);
     const ChunkBufs cb = chunk_bufs(sm, t & 1);
@@ -1502,6 +1515,11 @@ __device__ __forceinline__ void loader_loop(PrefillSmem& sm, const PrefillArgs& 
         *reinterpret_cast<u32x4*>(gate_unit<PrefillSmem>(cb, e - kTileUnits)) = tv[it];
       }
     }
+    if (deep && t + 2 < nchunks) {  // chunk t + 2's images into this set
+      const u32x4* src = tiles + int64_t(t + 2) * p.Hv * kTileImage;
+#pragma unroll
+      for (int it = 0; it < NTIT; ++it) tv[it] = src[toff[it]];
+    }
     clk.lap(7);
     if (t >= 1) wait_count<V::kHooks>(sm, kVFree, V::NCW * t);  // the consumers' last read of V
     clk.lap(8);
@@ -1512,10 +1530,12 @@ __device__ __forceinline__ void loader_loop(PrefillSmem& sm, const PrefillArgs& 
         *reinterpret_cast<u32x4*>(sm.V + (seg / (V::ROWS / 8)) * VSTR + 8 * (seg % (V::ROWS / 8))) = fv[it];
     }
     signal_count(sm, kReady, lane);
-    if (t + 1 < nchunks) {  // chunk t + 1's images and V slice into registers
-      const u32x4* src = tiles + int64_t(t + 1) * p.Hv * kTileImage;
+    if (t + 1 < nchunks) {  // chunk t + 1's V slice (and images) into registers
+      if (!deep) {
+        const u32x4* src = tiles + int64_t(t + 1) * p.Hv * kTileImage;
 #pragma unroll
-      for (int it = 0; it < NTIT; ++it) tv[it] = src[toff[it]];
+        for (int it = 0; it < NTIT; ++it) tv[it] = src[toff[it]];
+      }
       const uint16_t* vb = p.v + (ncs * p.Hv + h) * D + row0;
 #pragma unroll
       for (int it = 0; it < NVIT; ++it) {
@@ -1524,6 +1544,14 @@ __device__ __forceinline__ void loader_loop(PrefillSmem& sm, const PrefillArgs& 
       }
     }
     clk.lap(9);
+  };
+  if constexpr (deep) {
+    for (int t = 0; t < nchunks; t += 2) {
+      tick(t, tva);
+      if (t + 1 < nchunks) tick(t + 1, tvb);
+    }
+  } else {
+    for (int t = 0; t < nchunks; ++t) tick(t, tva);
   }
   clk.store(V::NCW + pw, lane0);
 }
@@ -2616,6 +2644,8 @@ int64_t prefill_work_items(int64_t chains) {
 namespace {
 // Largest workspace the two-kernel path uses; bigger batches take one kernel.
 constexpr int64_t kMaxWorkspaceBytes = int64_t(2) << 30;
+// Images above this size are read back mostly from HBM by the state pass.
+constexpr int64_t kDeepImageBytes = int64_t(96) << 20;
 }  // namespace
 
 // Batches split 4 or 8 ways repeat the producer work in every slice of a chain and
@@ -2659,6 +2689,12 @@ hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream, hipEvent_t d
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     if (F == 4) return launch_variant<Variant<2, 1, false, true>>(a, stream, done);
+    // Split 8 ways, images beyond what the caches keep between the two kernels are
+    // loaded two chunks ahead (one sequence of 8,192 tokens, 116 MB of images: 283 ->
+    // 272 us; 16,384 tokens 609 -> 581 us; 6,000 tokens, 85 MB: 188 -> 190 us).  Split
+    // 4 ways it measured no change (two 4,096-token sequences: 186.2 -> 185.8 us).
+    if (prefill_workspace_bytes(a.N, a.T, a.Hv) > kDeepImageBytes)
+      return launch_variant<Variant<4, 1, false, true, 4, false, true, true>>(a, stream, done);
     return launch_variant<Variant<4, 1, false, true, 4, false, true>>(a, stream, done);
   }
   // Split chains use 16-row consumer waves (VT = 1), whose per-chunk chain is

@@ -358,6 +358,7 @@ def _prefill_capi(p, gpu, workspace, ws=None, nbytes=None):
     ([1, 2, 63, 64, 129], Heads(2, 2, 4)),       # boundary lengths (chunk runs of 1 in the prep)
     ([700, 1300], Heads(8, 8, 16)),              # runs of several chunks per prep workgroup
     ([1000], Heads(16, 8, 32)),                  # distinct q and k head ratios, split 8 ways
+    ([3000, 2000], Heads(16, 16, 32)),           # 64 chains over 144 MB of images
 ])
 def test_prefill_two_kernel_path(gpu, lens, heads):
     """Batches of at most 64 chains with a workspace: a first kernel prepares every
@@ -610,13 +611,13 @@ def test_prefill_dropin_scratch_path(gpu, in_place):
 
 
 def test_prefill_dropin_long_sequence(gpu):
-    """A 6,000-token sequence (32 v-heads: 85 MB of chunk images, more than 64 MiB) runs
-    two kernels in the drop-in's scratch: against the oracle, and bit for bit equal to
-    gdn_prefill_with_workspace."""
-    say("prefill drop-in, one 6,000-token sequence")
+    """An 8,192-token sequence (32 v-heads: 116 MB of chunk images, more than 64 MiB, and
+    loaded two chunks ahead by the state pass) runs two kernels in the drop-in's scratch:
+    against the oracle, and bit for bit equal to gdn_prefill_with_workspace."""
+    say("prefill drop-in, one 8,192-token sequence")
     lib = _lib.load()
-    p = workloads.prefill_inputs([6000], seed=62, gate="slow", state_scale=0.5)
-    need = lib.gdn_prefill_workspace_size(1, 6000, 32)
+    p = workloads.prefill_inputs([8192], seed=62, gate="slow", state_scale=0.5)
+    need = lib.gdn_prefill_workspace_size(1, 8192, 32)
     assert 64 << 20 < need <= _lib.GDN_PREFILL_DROPIN_SCRATCH_BYTES, need
     o_ref, s_ref = oracle_prefill(p)
     out, ns = run_prefill(p, gpu)
