@@ -213,6 +213,34 @@ def bench_decode(args, torch, binding, workloads):
                 eager_ev_ms=ev_ms_e)
 
 
+DECODE_B1_BUFFERS = 192   # 192 x 2 MiB B=1 states (403 MB) rotate past the 256 MB Infinity Cache
+
+
+def bench_decode_b1(args, torch, binding, workloads):
+    """Single-sequence decode latency on BASELINE config 0's shape (B=1, heads 16/16/32,
+    fp32 state updated in place), graph-replayed: "cold" rotates over DECODE_B1_BUFFERS
+    independent states so each launch reads its state from HBM; "warm" reuses one state,
+    which then stays in the caches."""
+    dev = torch.device("cuda:0")
+    w = workloads.decode_inputs(1, seed=0, device=dev)
+    states = [w["state"]] + [w["state"].clone() for _ in range(DECODE_B1_BUFFERS - 1)]
+    out = torch.empty_like(w["v"])
+
+    def run(st):
+        binding.decode_kernel(w["q"], w["k"], w["v"], st, w["A_log"], w["a"], w["dt_bias"],
+                              w["b"], w["scale"], out, st)
+
+    steps = max(args.steps, 50)
+    _, cold_ms, mode = timed_launches(lambda i: run(states[i % DECODE_B1_BUFFERS]), steps,
+                                      args.warmup, torch, use_graph=True)
+    _, warm_ms, _ = timed_launches(lambda i: run(states[0]), steps, args.warmup, torch,
+                                   use_graph=True)
+    return {"us": round(cold_ms * 1e3, 3), "us_warm": round(warm_ms * 1e3, 3), "launch": mode,
+            "bytes": decode_bytes(1),
+            "gbs": round(decode_bytes(1) / (cold_ms * 1e-3) / 1e9, 1),
+            "state_buffers": DECODE_B1_BUFFERS}
+
+
 def bench_pooled(args, torch, binding, workloads):
     dev = torch.device("cuda:0")
     w = workloads.decode_inputs(512, seed=2, device=dev, pool_slots=1024)
@@ -229,22 +257,35 @@ def bench_pooled(args, torch, binding, workloads):
                 frac=nbytes / (ev_mean * 1e-3) / 1e9 / HBM_PEAK_GBS, bytes=nbytes)
 
 
-def bench_prefill(args, torch, binding, workloads, cfg, path="drop-in"):
+# Independent input/output/state sets that cold prefill timing rotates over, so that
+# the 256 MB Infinity Cache cannot serve a launch its inputs: config 4 (942 MB a set)
+# and config 3 (103 MB a set, plus the drop-in's 58 MB of chunk images, which every
+# launch rewrites before it reads them).
+PREFILL_COLD_SETS = {4: 3, 3: 4}
+
+
+def bench_prefill(args, torch, binding, workloads, cfg, path="drop-in", cold=False):
     """Prefill on config ``cfg`` through ``path``: "drop-in" (the reference-signature
     ``kernel``, gdn_prefill), "workspace" (gdn_prefill_with_workspace with a
     preallocated workspace) or "no-alloc" (gdn_prefill_no_alloc, the library's
-    scratch)."""
+    scratch).  Warm (default): every launch reuses one input/output/state set.  Cold
+    (drop-in only): launches rotate over PREFILL_COLD_SETS[cfg] sets with distinct
+    seeds."""
     dev = torch.device("cuda:0")
-    p = workloads.config(cfg, device=dev)
-    T = p["q"].shape[0]
-    N = p["cu_seqlens"].numel() - 1
-    out = torch.empty((T, HV, D), dtype=torch.bfloat16, device=dev)
-    ns = torch.empty((N, HV, D, D), dtype=torch.float32, device=dev)
-    args_ = (p["q"], p["k"], p["v"], p["state"], p["A_log"], p["a"], p["dt_bias"], p["b"],
-             p["cu_seqlens"], p["scale"], out, ns)
+    nsets = PREFILL_COLD_SETS[cfg] if cold else 1
+    sets = []
+    for j in range(nsets):
+        p = workloads.config(cfg, device=dev, seed=cfg + 100 * j)
+        T = p["q"].shape[0]
+        N = p["cu_seqlens"].numel() - 1
+        out = torch.empty((T, HV, D), dtype=torch.bfloat16, device=dev)
+        ns = torch.empty((N, HV, D, D), dtype=torch.float32, device=dev)
+        sets.append((p["q"], p["k"], p["v"], p["state"], p["A_log"], p["a"], p["dt_bias"], p["b"],
+                     p["cu_seqlens"], p["scale"], out, ns))
+    args_ = sets[0]
     if path == "drop-in":
         def step(i):
-            binding.prefill_kernel(*args_)
+            binding.prefill_kernel(*sets[i % nsets])
     elif path == "workspace":
         ws = torch.empty(binding.prefill_workspace_bytes(N, T, HV), dtype=torch.uint8, device=dev)
 
@@ -252,6 +293,7 @@ def bench_prefill(args, torch, binding, workloads, cfg, path="drop-in"):
             binding.prefill_kernel_with_workspace(*args_, ws)
     else:
         from gdn_kernel_amd import _lib
+        out, ns = args_[10], args_[11]
         lib = _lib.load()
         ptr = lambda t: None if t is None else t.data_ptr()
         cargs = [ptr(p[k]) for k in ("q", "k", "v", "state", "A_log", "a", "dt_bias", "b")]
@@ -275,9 +317,12 @@ def bench_prefill(args, torch, binding, workloads, cfg, path="drop-in"):
     wall, ev_mean, _ = timed_launches(step, steps, 0, torch)
     flop = HV * T * PREFILL_FLOP_PER_TOKEN_HEAD
     tfs = flop / (ev_mean * 1e-3) / 1e12
-    return dict(tokens=T, seqs=N, us=ev_mean * 1e3, tokens_per_s=T / (ev_mean * 1e-3),
-                tflops=tfs, mfma_frac=tfs / MFMA_BF16_PEAK_TFS, flop=flop,
-                lengths=p["lengths"] if cfg == 4 else None)
+    r = dict(tokens=T, seqs=N, us=ev_mean * 1e3, tokens_per_s=T / (ev_mean * 1e-3),
+             tflops=tfs, mfma_frac=tfs / MFMA_BF16_PEAK_TFS, flop=flop,
+             lengths=p["lengths"] if cfg == 4 else None)
+    if cold:
+        r["input_sets"] = nsets
+    return r
 
 
 def cpu_model():
@@ -438,11 +483,16 @@ def main():
         pooled = bench_pooled(args, torch, binding, workloads)
         res["decode_pooled_b512"] = {k: (round(v, 4) if isinstance(v, float) else v)
                                      for k, v in pooled.items()}
+        res["decode_b1"] = bench_decode_b1(args, torch, binding, workloads)
+        res["decode_b1_us"] = res["decode_b1"]["us"]
     if args.only in ("prefill", "all"):
-        for cfg, key, path in ((4, "prefill_varlen_32k", "drop-in"), (3, "prefill_t4096", "drop-in"),
-                               (3, "prefill_t4096_workspace", "workspace"),
-                               (3, "prefill_t4096_no_alloc", "no-alloc")):
-            pr = bench_prefill(args, torch, binding, workloads, cfg, path)
+        for cfg, key, path, cold in ((4, "prefill_varlen_32k", "drop-in", False),
+                                     (4, "prefill_varlen_32k_cold", "drop-in", True),
+                                     (3, "prefill_t4096", "drop-in", False),
+                                     (3, "prefill_t4096_cold", "drop-in", True),
+                                     (3, "prefill_t4096_workspace", "workspace", False),
+                                     (3, "prefill_t4096_no_alloc", "no-alloc", False)):
+            pr = bench_prefill(args, torch, binding, workloads, cfg, path, cold)
             pr["path"] = {"drop-in": "kernel (gdn_prefill, as the TVM-FFI shim)",
                           "workspace": "kernel_with_workspace (gdn_prefill_with_workspace)",
                           "no-alloc": "gdn_prefill_no_alloc (library scratch)"}[path]
@@ -457,8 +507,8 @@ def main():
     res["measured_peaks"] = peaks
     if "roofline" in res:
         res["roofline"]["frac_of_measured_copy"] = round(res["roofline"]["achieved"] / peaks["copy_gbs"], 4)
-    for key in ("prefill_varlen_32k", "prefill_t4096", "prefill_t4096_workspace",
-                "prefill_t4096_no_alloc"):
+    for key in ("prefill_varlen_32k", "prefill_varlen_32k_cold", "prefill_t4096",
+                "prefill_t4096_cold", "prefill_t4096_workspace", "prefill_t4096_no_alloc"):
         if key in res:
             res[key]["frac_of_measured_gemm"] = round(res[key]["tflops"] / peaks["bf16_gemm_tflops"], 4)
     if not args.no_cpu:

@@ -20,7 +20,7 @@ GDN_INDEX_INT32 = 0
 GDN_INDEX_INT64 = 1
 GDN_MAX_HEADS = 65536
 GDN_PREFILL_NO_ALLOC_SCRATCH_BYTES = 64 << 20
-GDN_PREFILL_DROPIN_SCRATCH_BYTES = 256 << 20
+GDN_PREFILL_DROPIN_SCRATCH_BYTES = 128 << 20
 
 # Exported symbols and their argument types (must match include/gdn_kernel_amd.h and
 # include/gdn_kernel_amd_testing.h).
@@ -44,6 +44,8 @@ SIGNATURES = {
     "gdn_prefill_with_workspace": ([_P] * 8 + [_P, c_int32, c_int64, c_int64, c_double, _P, _P]
                                    + _HEADS + [_P, c_int64, _P], c_int),
     "gdn_prefill_giveups": ([ctypes.POINTER(ctypes.c_uint64), c_int32], c_int),
+    "gdn_decode_pool_conflicts": ([ctypes.POINTER(ctypes.c_uint64), c_int32], c_int),
+    "gdn_static_device_bytes": ([], c_int64),
     "gdn_prefill_no_alloc": ([_P] * 8 + [_P, c_int32, c_int64, c_int64, c_double, _P, _P] + _HEADS
                              + [_P], c_int),
     # include/gdn_kernel_amd_testing.h

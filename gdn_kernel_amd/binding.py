@@ -34,7 +34,7 @@ import torch
 from . import _lib
 
 __all__ = ["decode_kernel", "decode_pooled_kernel", "prefill_kernel", "prefill_kernel_with_workspace",
-           "prefill_workspace_bytes", "prefill_giveups", "GDNError"]
+           "prefill_workspace_bytes", "prefill_giveups", "decode_pool_conflicts", "GDNError"]
 
 GDNError = _lib.GDNError
 _BF16 = torch.bfloat16
@@ -136,8 +136,9 @@ def decode_pooled_kernel(q, k, v, state_pool, A_log, a, dt_bias, b, scale, outpu
                          state_indices) -> None:
     """Decode step with the state of batch row i held in ``state_pool[state_indices[i]]``
     (updated in place).  state_pool [S,Hv,128,128] fp32; state_indices [B] int32;
-    an index outside [0, S) is a padding row (zero output, no slot touched).
-    Valid indices must be distinct."""
+    an index outside [0, S) is a padding row (zero output, no slot touched).  Rows
+    whose slot another row of the batch also names are skipped the same way, on the
+    device, and counted (``decode_pool_conflicts``)."""
     dev = _device_of(q)
     if q.dim() != 4 or k.dim() != 4 or v.dim() != 4:
         raise ValueError("q, k, v must be 4-D [B, 1, H, d]")
@@ -273,5 +274,20 @@ def prefill_giveups(reset: bool = False, device=None) -> int:
     count = ctypes.c_uint64(0)
     with _on_device(dev):
         rc = lib.gdn_prefill_giveups(ctypes.byref(count), 1 if reset else 0)
+    _lib.check(rc)
+    return int(count.value)
+
+
+def decode_pool_conflicts(reset: bool = False, device=None) -> int:
+    """Number of pooled-decode rows on ``device`` (default: the current one) skipped
+    because another row of their batch named the same state slot, since the library
+    was loaded or the last reset (gdn_decode_pool_conflicts).  Synchronises the
+    device.  A skipped row's output is zero and its slot is left as it was."""
+    import ctypes
+    lib = _lib.load()
+    dev = torch.device("cuda", torch.cuda.current_device()) if device is None else torch.device(device)
+    count = ctypes.c_uint64(0)
+    with _on_device(dev):
+        rc = lib.gdn_decode_pool_conflicts(ctypes.byref(count), 1 if reset else 0)
     _lib.check(rc)
     return int(count.value)

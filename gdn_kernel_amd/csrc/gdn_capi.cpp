@@ -237,13 +237,18 @@ int decode_pooled_impl(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v, 
                        "gdn_decode_pooled launch");
 }
 
+// Launcher of a prefill call: launch_prefill (optionally with a caller workspace),
+// the drop-in's (its own ordered scratch for one long sequence) or
+// gdn_prefill_no_alloc's (the library's ordered scratch).
+enum class PrefillPath { kPlain, kDropin, kNoAlloc };
+
 int prefill_impl(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v, const float* state, const float* A_log,
                  const gdn_bf16* a, const float* dt_bias, const gdn_bf16* b, const void* cu_seqlens,
                  int32_t cu_seqlens_dtype, int64_t num_seqs, int64_t total_tokens, double scale, gdn_bf16* output,
                  float* new_state, int32_t num_q_heads, int32_t num_k_heads, int32_t num_v_heads,
                  int32_t head_dim_k, int32_t head_dim_v, int32_t spin_limit, int32_t ready_chunks,
                  uint32_t* aborts, void* workspace, int64_t workspace_bytes, void* stream,
-                 bool dropin = false) {
+                 PrefillPath path = PrefillPath::kPlain) {
   GDN_TRY(gdn_prefill_check(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu_seqlens_dtype, num_seqs,
                             total_tokens, scale, output, new_state, num_q_heads, num_k_heads, num_v_heads,
                             head_dim_k, head_dim_v));
@@ -274,8 +279,10 @@ int prefill_impl(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v, const 
   args.T = total_tokens;
   args.N = int(num_seqs); args.Hq = num_q_heads; args.Hk = num_k_heads; args.Hv = num_v_heads;
   const hipStream_t st = static_cast<hipStream_t>(stream);
-  return device_status(dropin ? gdn::launch_prefill_dropin(args, st) : gdn::launch_prefill(args, st),
-                       "gdn_prefill launch");
+  const hipError_t e = path == PrefillPath::kDropin   ? gdn::launch_prefill_dropin(args, st)
+                       : path == PrefillPath::kNoAlloc ? gdn::launch_prefill_no_alloc(args, st)
+                                                       : gdn::launch_prefill(args, st);
+  return device_status(e, "gdn_prefill launch");
 }
 
 int check_variant(int32_t variant) {
@@ -312,7 +319,7 @@ int gdn_prefill(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v, const f
                 int32_t head_dim_k, int32_t head_dim_v, void* stream) {
   return prefill_impl(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu_seqlens_dtype, num_seqs, total_tokens,
                       scale, output, new_state, num_q_heads, num_k_heads, num_v_heads, head_dim_k, head_dim_v, 0, 0,
-                      nullptr, nullptr, 0, stream, true);
+                      nullptr, nullptr, 0, stream, PrefillPath::kDropin);
 }
 
 int64_t gdn_prefill_workspace_size(int64_t num_seqs, int64_t total_tokens, int32_t num_v_heads) {
@@ -346,16 +353,23 @@ int gdn_prefill_no_alloc(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v
                 "this batch needs %lld bytes of chunk images, more than the %lld-byte scratch of "
                 "gdn_prefill_no_alloc; use gdn_prefill_with_workspace (or gdn_prefill)",
                 static_cast<long long>(need), static_cast<long long>(gdn::kPrefillScratchBytes));
-  void* ws = nullptr;
-  if (need > 0) GDN_TRY(device_status(gdn::prefill_scratch(&ws), "gdn_prefill_no_alloc: scratch address"));
   return prefill_impl(q, k, v, state, A_log, a, dt_bias, b, cu_seqlens, cu_seqlens_dtype, num_seqs, total_tokens,
                       scale, output, new_state, num_q_heads, num_k_heads, num_v_heads, head_dim_k, head_dim_v, 0, 0,
-                      nullptr, ws, need, stream);
+                      nullptr, nullptr, 0, stream, PrefillPath::kNoAlloc);
+}
+
+int64_t gdn_static_device_bytes(void) {
+  return gdn::prefill_static_device_bytes() + gdn::decode_static_device_bytes();
 }
 
 int gdn_prefill_giveups(uint64_t* count, int32_t reset) {
   if (!count) return fail(GDN_ERR_INVALID_ARGUMENT, "count must not be null");
   return device_status(gdn::prefill_giveups(count, reset != 0), "gdn_prefill_giveups");
+}
+
+int gdn_decode_pool_conflicts(uint64_t* count, int32_t reset) {
+  if (!count) return fail(GDN_ERR_INVALID_ARGUMENT, "count must not be null");
+  return device_status(gdn::decode_pool_conflicts(count, reset != 0), "gdn_decode_pool_conflicts");
 }
 
 int gdn_decode_num_variants(void) { return gdn::kDecodeVariants; }

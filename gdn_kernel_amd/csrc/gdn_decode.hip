@@ -25,6 +25,11 @@ namespace gdn {
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 
+// Rows of pooled decode launches on this device skipped because another row of the
+// same batch named their slot, since the library was loaded or the count was last
+// reset; read by decode_pool_conflicts.
+__device__ unsigned long long gdn_decode_pool_conflict_count;
+
 template <bool NT>
 __device__ __forceinline__ float4 load_state(const float* p) {
   f32x4 v;
@@ -43,6 +48,39 @@ __device__ __forceinline__ void store_state(float* p, float4 x) {
     __builtin_nontemporal_store(v, reinterpret_cast<f32x4*>(p));
   } else {
     *reinterpret_cast<f32x4*>(p) = v;
+  }
+}
+
+// Whether a row other than `bi` of the batch's B slot indices names `slot`.  The
+// WAVES waves of a workgroup (all on the same batch row) each scan an interleaved
+// share of the indices, four 64-index blocks per pass, and OR their verdicts
+// through LDS.  Ends with a workgroup barrier when WAVES > 1.
+template <int WAVES>
+__device__ __forceinline__ bool slot_named_elsewhere(const int32_t* slots, int B, int bi, int slot, int lane,
+                                                     int wave) {
+  constexpr int STEP = 64 * WAVES;
+  bool hit = false;
+  for (int i0 = 64 * wave; i0 < B; i0 += 4 * STEP) {
+    int s[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      const int i = i0 + u * STEP + lane;
+      s[u] = i < B ? slots[i] : -1;
+    }
+#pragma unroll
+    for (int u = 0; u < 4; ++u) hit |= s[u] == slot && i0 + u * STEP + lane != bi;
+  }
+  const bool any = __builtin_amdgcn_ballot_w64(hit) != 0;
+  if constexpr (WAVES == 1) {
+    return any;
+  } else {
+    __shared__ int wave_hit[WAVES];
+    if (lane == 0) wave_hit[wave] = any;
+    __syncthreads();
+    int r = 0;
+#pragma unroll
+    for (int w = 0; w < WAVES; ++w) r |= wave_hit[w];
+    return r != 0;
   }
 }
 
@@ -76,6 +114,15 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_decode_kernel(DecodeArgs p) {
     const int64_t slot = p.slots[bi];
     if (slot < 0 || slot >= p.pool_slots) {         // padding slot: zero output, no state
       if (lane < RPW) outp[lane] = 0;
+      return;
+    }
+    // A slot that two rows of the batch name would be updated by both at once: such
+    // rows are skipped like padding (zero output, slot untouched), decided before any
+    // state access, and the first wave of each counts its row once.
+    if (slot_named_elsewhere<WAVES>(p.slots, p.B, bi, int(slot), lane, wave)) {
+      if (lane < RPW) outp[lane] = 0;
+      if (h == 0 && row0 == 0 && lane == 0)
+        __hip_atomic_fetch_add(&gdn_decode_pool_conflict_count, 1ull, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
       return;
     }
     shead = slot * p.Hv + h;
@@ -174,6 +221,22 @@ int64_t decode_items_per_head(int variant) {
     default:
       return kHeadDim / 16 * 64;
   }
+}
+
+int64_t decode_static_device_bytes() { return int64_t(sizeof(gdn_decode_pool_conflict_count)); }
+
+hipError_t decode_pool_conflicts(uint64_t* count, bool reset) {
+  hipError_t e = hipDeviceSynchronize();
+  if (e != hipSuccess) return e;
+  unsigned long long v = 0;
+  e = hipMemcpyFromSymbol(&v, HIP_SYMBOL(gdn_decode_pool_conflict_count), sizeof(v));
+  if (e != hipSuccess) return e;
+  *count = v;
+  if (reset) {
+    const unsigned long long z = 0;
+    e = hipMemcpyToSymbol(HIP_SYMBOL(gdn_decode_pool_conflict_count), &z, sizeof(z));
+  }
+  return e;
 }
 
 hipError_t launch_decode(const DecodeArgs& a, hipStream_t stream, int variant) {

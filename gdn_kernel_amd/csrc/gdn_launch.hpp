@@ -66,6 +66,11 @@ hipError_t launch_decode(const DecodeArgs& args, hipStream_t stream, int variant
 int decode_pick_variant(int64_t heads);
 int64_t decode_items_per_head(int variant);
 
+// Rows of pooled decode launches on the current device that were skipped because
+// another row of their batch named the same slot, since the library was loaded or
+// the last reset; synchronises the device first.
+hipError_t decode_pool_conflicts(uint64_t* count, bool reset);
+
 // Work-items of a prefill main-kernel launch for this many (sequence, v-head)
 // chains on the current device (the grid times the workgroup size of the variant
 // the launcher picks).
@@ -82,9 +87,19 @@ hipError_t prefill_scratch(void** ptr);
 // The drop-in gdn_prefill's launcher: launch_prefill, except that one sequence of at
 // least kDropinTwoKernelTokens tokens runs the two-kernel path in a per-device scratch
 // of the library (kPrefillDropinScratchBytes), ordered between launches by an event.
-constexpr int64_t kPrefillDropinScratchBytes = int64_t(256) << 20;
+constexpr int64_t kPrefillDropinScratchBytes = int64_t(128) << 20;
 constexpr int64_t kDropinTwoKernelTokens = 1024;
 hipError_t launch_prefill_dropin(const PrefillArgs& args, hipStream_t stream);
+
+// gdn_prefill_no_alloc's launcher: the two-kernel path (for batches that take it) in
+// the kPrefillScratchBytes array; eager launches are ordered between each other by an
+// event, like the drop-in's.  The caller has checked that the images fit.
+hipError_t launch_prefill_no_alloc(const PrefillArgs& args, hipStream_t stream);
+
+// Device memory the library holds on every device its code is loaded onto, from load
+// until the process ends: the two prefill scratch arrays and the device counters.
+int64_t prefill_static_device_bytes();
+int64_t decode_static_device_bytes();
 
 // Waves of prefill launches on the current device whose hand-off wait gave up,
 // since the library was loaded or the last reset; synchronises the device first.

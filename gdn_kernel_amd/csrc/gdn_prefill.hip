@@ -190,6 +190,13 @@ struct __align__(16) PrefillSmem {
   unsigned* aborts;           // kernels with testing hooks: optional count of waits that gave up
 };
 
+// Before a workgroup's first chunk its LDS tiles double as integer scratch: the
+// longest-first ranking (pick_sequence) keeps up to kMaxSortedSeqs lengths in Nh, and
+// the persistent kernel's boustrophedon lists keep lengths, starts and order of up to
+// kMaxSortedSeqs sequences in V.
+static_assert(kMaxSortedSeqs * sizeof(int) <= sizeof(PrefillSmem::Nh), "sequence lengths fit Nh");
+static_assert(3 * kMaxSortedSeqs * sizeof(int) <= sizeof(PrefillSmem::V), "sequence lists fit V");
+
 // The token-split state pass exchanges Y and the state's bf16 hi/lo parts through
 // Nh/Nl (unused without producers): four 16-token blocks of Y and four 32-column
 // blocks of the state, 16 and 32 bytes per lane.
@@ -2513,8 +2520,68 @@ int device_cus() {
 // copy until the process ends; every call on a device shares it.
 static __device__ __align__(256) uint8_t scratch[kPrefillScratchBytes];
 
+// Scratch of the drop-in gdn_prefill's two-kernel path (one long sequence, below):
+// its own array, so that no call of gdn_prefill_no_alloc, captured or not, shares it.
+static __device__ __align__(256) uint8_t dropin_scratch[kPrefillDropinScratchBytes];
+
 namespace {
 constexpr int kMaxDevices = 64;
+
+// Per device and scratch array: the array's device address (looked up once, with
+// the device current: in host code the array's name is a host-side stand-in), the
+// event that follows the last launch using it, and the lock that orders the
+// check-launch-record sequence between host threads.  Created on first use and
+// kept until the process ends, like the array itself.
+struct OrderedScratch {
+  std::mutex lock;
+  void* addr = nullptr;
+  hipEvent_t done = nullptr;
+  bool used = false;
+};
+OrderedScratch g_dropin[kMaxDevices];
+OrderedScratch g_no_alloc[kMaxDevices];
+
+// Launches the two-kernel path of `a` with its chunk images in the scratch array
+// `symbol`, ordered after the previous launch that used the array on this device:
+// the stream waits for that launch's event, and the state pass records the event
+// again as it completes.  If the launch fails after the prep kernel was enqueued,
+// the event is recorded behind it all the same, so the next launch still waits for
+// the orphaned kernel.
+hipError_t launch_ordered(const PrefillArgs& a, hipStream_t stream, OrderedScratch* table, const void* symbol) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
+  OrderedScratch& d = table[dev];
+  std::lock_guard<std::mutex> guard(d.lock);
+  if (d.addr == nullptr) {
+    e = hipGetSymbolAddress(&d.addr, symbol);
+    if (e != hipSuccess) return e;
+  }
+  if (d.done == nullptr) {
+    e = hipEventCreate(&d.done);
+    if (e != hipSuccess) return e;
+  }
+  if (d.used) {
+    e = hipStreamWaitEvent(stream, d.done, 0);
+    if (e != hipSuccess) return e;
+  }
+  PrefillArgs b = a;
+  b.tiles = static_cast<uint16_t*>(d.addr);
+  e = launch_prefill(b, stream, d.done);  // the state pass records `done` as it completes
+  if (e != hipSuccess) {
+    (void)hipGetLastError();
+    (void)hipEventRecord(d.done, stream);
+  }
+  d.used = true;
+  return e;
+}
+
+bool stream_capturing(hipStream_t stream, hipError_t* err) {
+  hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
+  *err = hipStreamIsCapturing(stream, &capture);
+  return *err == hipSuccess && capture != hipStreamCaptureStatusNone;
+}
 }  // namespace
 
 // The device address of `scratch` on the current device, looked up once per
@@ -2536,65 +2603,46 @@ hipError_t prefill_scratch(void** ptr) {
   return hipSuccess;
 }
 
-// Scratch of the drop-in gdn_prefill's two-kernel path (one long sequence, below):
-// its own array, so that no call of gdn_prefill_no_alloc, captured or not, shares it.
-static __device__ __align__(256) uint8_t dropin_scratch[kPrefillDropinScratchBytes];
-
-namespace {
-
-// Per device: the event that follows the last drop-in launch using dropin_scratch,
-// and the lock that orders the check-launch-record sequence between host threads.
-// The address and the event are created on first use and kept until the process
-// ends, like the scratch itself.
-struct DropinScratch {
-  std::mutex lock;
-  void* addr = nullptr;
-  hipEvent_t done = nullptr;
-  bool used = false;
-};
-DropinScratch g_dropin[kMaxDevices];
-
-}  // namespace
+int64_t prefill_static_device_bytes() {
+  return int64_t(sizeof(scratch)) + int64_t(sizeof(dropin_scratch)) + int64_t(sizeof(gdn_prefill_giveup_count));
+}
 
 // The drop-in gdn_prefill.  One sequence of at least kDropinTwoKernelTokens tokens,
 // whose chains the launcher splits 4 or 8 ways, runs on the two-kernel path (each
 // chunk prepared once) in dropin_scratch when its images fit; everything else, and
 // any launch on a stream that is being captured into a graph, runs launch_prefill as
-// is.  Launches on the scratch are ordered on the device: each waits (on its stream)
-// for the event recorded after the previous one, so calls on any streams stay
-// correct, and calls on one stream wait for nothing they would not wait for anyway.
+// is.  Launches on the scratch are ordered on the device (launch_ordered), so calls on
+// any streams stay correct, and calls on one stream wait for nothing they would not
+// wait for anyway.
 hipError_t launch_prefill_dropin(const PrefillArgs& a, hipStream_t stream) {
   const int64_t need = a.N == 1 && a.T >= kDropinTwoKernelTokens ? prefill_workspace_bytes(a.N, a.T, a.Hv) : 0;
   if (need <= 0 || need > kPrefillDropinScratchBytes || a.spin_limit != 0 || a.ready_chunks != 0 ||
       a.aborts != nullptr || a.tiles != nullptr)
     return launch_prefill(a, stream);
-  hipStreamCaptureStatus capture = hipStreamCaptureStatusNone;
-  hipError_t e = hipStreamIsCapturing(stream, &capture);
+  hipError_t e = hipSuccess;
+  if (stream_capturing(stream, &e)) return launch_prefill(a, stream);
   if (e != hipSuccess) return e;
-  if (capture != hipStreamCaptureStatusNone) return launch_prefill(a, stream);
-  int dev = 0;
-  e = hipGetDevice(&dev);
+  return launch_ordered(a, stream, g_dropin, HIP_SYMBOL(dropin_scratch));
+}
+
+// gdn_prefill_no_alloc: the two-kernel path in `scratch` for batches that take it.
+// On a stream that is not being captured, launches are ordered on the device like
+// the drop-in's (their own event), so eager calls on any streams stay correct.  A
+// launch captured into a graph cannot wait for that event: its replays and any other
+// use of the array on the device must not overlap.
+hipError_t launch_prefill_no_alloc(const PrefillArgs& a, hipStream_t stream) {
+  const int64_t need = prefill_workspace_bytes(a.N, a.T, a.Hv);
+  if (need <= 0) return launch_prefill(a, stream);
+  if (need > kPrefillScratchBytes) return hipErrorInvalidValue;
+  hipError_t e = hipSuccess;
+  if (stream_capturing(stream, &e)) {
+    PrefillArgs b = a;
+    e = prefill_scratch(reinterpret_cast<void**>(&b.tiles));
+    if (e != hipSuccess) return e;
+    return launch_prefill(b, stream);
+  }
   if (e != hipSuccess) return e;
-  if (dev < 0 || dev >= kMaxDevices) return hipErrorInvalidDevice;
-  DropinScratch& d = g_dropin[dev];
-  std::lock_guard<std::mutex> guard(d.lock);
-  if (d.addr == nullptr) {
-    e = hipGetSymbolAddress(&d.addr, HIP_SYMBOL(dropin_scratch));
-    if (e != hipSuccess) return e;
-  }
-  if (d.done == nullptr) {
-    e = hipEventCreate(&d.done);
-    if (e != hipSuccess) return e;
-  }
-  if (d.used) {
-    e = hipStreamWaitEvent(stream, d.done, 0);
-    if (e != hipSuccess) return e;
-  }
-  PrefillArgs b = a;
-  b.tiles = static_cast<uint16_t*>(d.addr);
-  e = launch_prefill(b, stream, d.done);  // the state pass records `done` as it completes
-  if (e == hipSuccess) d.used = true;
-  return e;
+  return launch_ordered(a, stream, g_no_alloc, HIP_SYMBOL(scratch));
 }
 
 // Reads (and with `reset` clears) this device's give-up count, after

@@ -6,8 +6,30 @@
  * passed as an opaque pointer (hipStream_t; NULL = the default stream).  All
  * tensors are dense row-major (C-contiguous) in the layouts documented per
  * function; bf16 tensors are raw 16-bit bf16 bit patterns.  Launches are
- * asynchronous on the given stream; no entry point synchronises, allocates
- * device memory or keeps state between calls.
+ * asynchronous on the given stream.
+ *
+ * Synchronisation, allocation and state (what each entry point does beyond its
+ * outputs):
+ *   - No entry point allocates device memory (no hipMalloc / hipFree, no library
+ *     routine that allocates).
+ *   - gdn_prefill_giveups and gdn_decode_pool_conflicts synchronise the current
+ *     device (hipDeviceSynchronize) before they read their device counter; no other
+ *     entry point synchronises the device, a stream or the host.
+ *   - Static device memory: every device the library's code is loaded onto holds,
+ *     from load until the process ends, gdn_static_device_bytes() bytes:
+ *     GDN_PREFILL_DROPIN_SCRATCH_BYTES (gdn_prefill's scratch) +
+ *     GDN_PREFILL_NO_ALLOC_SCRATCH_BYTES (gdn_prefill_no_alloc's) + 12 bytes of
+ *     device counters (192 MiB in all), whether or not a prefill ever runs.
+ *     Torch's allocator does not see it.
+ *   - Per-device host state: gdn_prefill and gdn_prefill_no_alloc each keep, per
+ *     device and for their own scratch array, the array's address, a mutex and one
+ *     event (created on first use and kept) that orders their two-kernel launches
+ *     on that device (each such launch waits, on its stream, for the event the
+ *     previous one recorded).  The two device counters (prefill hand-off give-ups,
+ *     pooled-decode slot conflicts) persist between calls until their query resets
+ *     them.  The decode entry points keep no other state.
+ *   - Thread safety: every entry point may be called from any host thread; the
+ *     per-device state above is guarded by its mutex.
  *
  * Return value: GDN_OK (0) on success, otherwise a GDN_ERR_* code; the
  * calling thread's gdn_last_error() then describes the failure.  Argument
@@ -87,8 +109,11 @@ int gdn_decode_check(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v,
  *   state_pool    [pool_slots,Hv,128,128] fp32 (read and written)
  *   state_indices [B] int32 device array; an index outside [0, pool_slots)
  *                 marks a padding row: its output is zero and no slot is touched.
- * Two valid rows naming the same slot race; callers must not do that.
- * Other arguments as gdn_decode.
+ * A slot that two or more valid rows name is a conflict: updating it from both rows
+ * would race.  The kernel detects it on the device before it touches any state
+ * (each row's workgroups scan the B indices) and skips every such row like a padding
+ * row (zero output, slot untouched); gdn_decode_pool_conflicts counts the skipped
+ * rows.  Other arguments as gdn_decode.
  */
 int gdn_decode_pooled(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v,
                       float* state_pool, int64_t pool_slots,
@@ -106,6 +131,18 @@ int gdn_decode_pooled_check(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16
                             int32_t num_q_heads, int32_t num_k_heads,
                             int32_t num_v_heads, int32_t head_dim_k,
                             int32_t head_dim_v);
+
+/*
+ * Conflict report of gdn_decode_pooled.  No reference counterpart (the reference has
+ * no pooled decode).  Synchronises the current device, stores in *count the number of
+ * pooled rows skipped because another row of their batch named the same slot (since
+ * the library was loaded, or since the last reset), and with reset != 0 clears it.
+ */
+int gdn_decode_pool_conflicts(uint64_t* count, int32_t reset);
+
+/* Bytes of device memory the library holds on each device its code is loaded onto
+ * (the scratch arrays and counters above), for memory accounting. */
+int64_t gdn_static_device_bytes(void);
 
 /*
  * Varlen chunked prefill (chunk 64), destination-passing.  Replaces the
@@ -127,14 +164,16 @@ int gdn_decode_pooled_check(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16
  * tokens, whose chains the launcher splits over several workgroups, runs the
  * two-kernel path of gdn_prefill_with_workspace (each chunk prepared once) in a
  * scratch array the library holds on each device (GDN_PREFILL_DROPIN_SCRATCH_BYTES,
- * its own, not gdn_prefill_no_alloc's; with 32 v-heads it holds the images of up
- * to 18,880 tokens), when its chunk images fit; the results are
- * the same bit for bit.  The library orders those launches on the device (each
+ * its own, not gdn_prefill_no_alloc's), when its chunk images fit: 28,416 bytes per
+ * 64-token chunk and v-head, so with 32 v-heads sequences of up to 9,408 tokens
+ * (BASELINE's 4,096-token sequence needs 55.5 MiB).  Longer sequences run one
+ * kernel (16,384 tokens: about 8 % slower than two).  The results are the same bit
+ * for bit either way.  The library orders those launches on the device (each
  * waits, on its stream, for an event that the previous one records as it
  * completes), so calls on any streams stay correct; on a stream that is being
  * captured into a graph such a call runs one kernel instead.
  */
-#define GDN_PREFILL_DROPIN_SCRATCH_BYTES (256LL << 20)
+#define GDN_PREFILL_DROPIN_SCRATCH_BYTES (128LL << 20)
 
 int gdn_prefill(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v,
                 const float* state, const float* A_log, const gdn_bf16* a,
@@ -193,8 +232,11 @@ int gdn_prefill_with_workspace(const gdn_bf16* q, const gdn_bf16* k, const gdn_b
  * per call.  A batch whose images need more than that (gdn_prefill_workspace_size
  * above it) returns GDN_ERR_INVALID_ARGUMENT; batches that gdn_prefill serves with
  * one kernel need no scratch.  Every call on a device shares that device's
- * scratch: calls that overlap on one GPU (launched on different streams without
- * ordering between them) race and give wrong results.
+ * scratch.  Calls on streams that are not being captured are ordered on the device
+ * like gdn_prefill's (their own mutex and event), so eager calls on any streams stay
+ * correct.  A call captured into a graph cannot wait for that event: its replays
+ * must not overlap with any other call of gdn_prefill_no_alloc on the same GPU
+ * (eager or replayed), or they race and give wrong results.
  */
 #define GDN_PREFILL_NO_ALLOC_SCRATCH_BYTES (64LL << 20)
 

@@ -150,16 +150,31 @@ def decode(q, k, v, state, A_log, a, dt_bias, b, scale, dtype=np.float64):
     return out[:, None], new_state
 
 
+def pool_conflicts(state_indices, pool_slots):
+    """Rows of a pooled decode batch whose in-range slot another row also names."""
+    idx = np.asarray(state_indices).astype(np.int64)
+    valid = (idx >= 0) & (idx < pool_slots)
+    if not valid.any():
+        return np.zeros(idx.shape, bool)
+    uniq, counts = np.unique(idx[valid], return_counts=True)
+    return valid & np.isin(idx, uniq[counts > 1])
+
+
 def decode_pooled(q, k, v, pool, state_indices, A_log, a, dt_bias, b, scale,
                   dtype=np.float64):
     """Decode over an indexed state pool: gather pool[idx[b]] -> decode ->
     scatter back.  No reference counterpart; the semantics
     are gather/decode/scatter.  Slots outside [0, pool_slots) are padding:
-    their output rows are zero and no pool slot is touched.  Untouched slots keep
-    their exact bits.  Returns (output, new_pool)."""
+    their output rows are zero and no pool slot is touched.  A slot that more than
+    one in-range row names is a conflict (updating it from each row would race):
+    every row naming it is treated as padding.  Untouched slots keep their exact
+    bits.  Returns (output, new_pool)."""
     pool = np.asarray(pool, dtype)
     idx = np.asarray(state_indices).astype(np.int64)
     valid = (idx >= 0) & (idx < pool.shape[0])
+    if valid.any():
+        uniq, counts = np.unique(idx[valid], return_counts=True)
+        valid &= ~np.isin(idx, uniq[counts > 1])
     B = q.shape[0]
     Hv, V = v.shape[2], v.shape[3]
     out = np.zeros((B, 1, Hv, V), dtype)

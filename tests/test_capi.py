@@ -275,3 +275,33 @@ def test_prefill_giveups_reporting(lib):
     else:
         assert "gdn_prefill_giveups" in _lib.last_error()
         assert count.value == 12345
+
+
+def test_decode_pool_conflicts_reporting(lib):
+    """gdn_decode_pool_conflicts (the device count of pooled decode rows skipped because
+    another row named their slot) rejects a null destination before any device call;
+    without a usable GPU it reports a device error and leaves the destination alone."""
+    assert lib.gdn_decode_pool_conflicts(None, 1) == INVALID
+    assert "count" in _lib.last_error()
+    count = ctypes.c_uint64(777)
+    rc = lib.gdn_decode_pool_conflicts(ctypes.byref(count), 0)
+    assert rc in (OK, _lib.GDN_ERR_DEVICE)
+    if rc != OK:
+        assert "gdn_decode_pool_conflicts" in _lib.last_error()
+        assert count.value == 777
+
+
+def test_static_device_bytes_match_the_header(lib):
+    """gdn_static_device_bytes (device memory the library holds on every device it is
+    loaded onto) is the two prefill scratch arrays the header names plus 12 bytes of
+    device counters (prefill give-ups, 4; pooled-decode conflicts, 8): 192 MiB."""
+    want = _lib.GDN_PREFILL_DROPIN_SCRATCH_BYTES + _lib.GDN_PREFILL_NO_ALLOC_SCRATCH_BYTES + 12
+    assert lib.gdn_static_device_bytes() == want
+    assert _lib.GDN_PREFILL_DROPIN_SCRATCH_BYTES == 128 << 20
+    assert _lib.GDN_PREFILL_NO_ALLOC_SCRATCH_BYTES == 64 << 20
+    assert want == (192 << 20) + 12
+    # the drop-in array holds config 3's images (one 4,096-token sequence, 32 v-heads)
+    # and those of one sequence of up to 9,408 tokens
+    assert lib.gdn_prefill_workspace_size(1, 4096, 32) <= _lib.GDN_PREFILL_DROPIN_SCRATCH_BYTES
+    assert lib.gdn_prefill_workspace_size(1, 9408, 32) <= _lib.GDN_PREFILL_DROPIN_SCRATCH_BYTES
+    assert lib.gdn_prefill_workspace_size(1, 9409, 32) > _lib.GDN_PREFILL_DROPIN_SCRATCH_BYTES

@@ -136,6 +136,43 @@ def test_decode_pooled_config2_full_size(gpu):
     assert torch.equal(pool[idx.long()], gathered)
 
 
+@pytest.mark.conflicts_expected
+@pytest.mark.parametrize("heads,B,slots", [((16, 16, 32), 12, 40), ((1, 1, 4), 20, 64),
+                                           ((1, 1, 4), 1500, 2048)])
+def test_decode_pooled_duplicate_slots(gpu, heads, B, slots):
+    """Rows naming a slot that another row also names: a pair at the first and last row
+    (the two ends of the index scan), a triple in the middle, plus a padding row.  Each
+    conflicting row has zero output and its slot keeps its bits; every other row matches
+    the oracle; gdn_decode_pool_conflicts counts the five skipped rows.  The layouts take
+    one-wave (B*Hv < 128) and four-wave workgroups, the last over several scan passes."""
+    say(f"decode pooled duplicate slots heads={heads} B={B} slots={slots}")
+    w = workloads.decode_inputs(B, Heads(*heads), seed=40 + B, gate="slow", pool_slots=slots,
+                                state_scale=1.0)
+    idx = w["state_indices"].clone()
+    mid = B // 2
+    idx[B - 1] = idx[0]
+    idx[mid + 1] = idx[mid]
+    idx[mid + 2] = idx[mid]
+    idx[1] = -1
+    conflict = O.pool_conflicts(idx.numpy(), slots)
+    assert int(conflict.sum()) == 5
+    o_ref, pool_ref = O.decode_pooled(*[to_numpy(w[k]) for k in ("q", "k", "v", "state")],
+                                      idx.numpy(), *[to_numpy(w[k]) for k in
+                                                     ("A_log", "a", "dt_bias", "b")], w["scale"])
+    d = {k: (v.to(gpu) if isinstance(v, torch.Tensor) else v) for k, v in w.items()}
+    pool = d["state"].clone()
+    out = torch.full_like(d["v"], float("nan"))
+    binding.decode_pool_conflicts(reset=True)
+    binding.decode_pooled_kernel(d["q"], d["k"], d["v"], pool, d["A_log"], d["a"], d["dt_bias"],
+                                 d["b"], d["scale"], out, idx.to(gpu))
+    assert binding.decode_pool_conflicts(reset=True) == 5
+    assert not host(out)[conflict].any()
+    assert_close(host(out), o_ref, OUT_RTOL, OUT_ATOL, "output")
+    shared = sorted(set(int(i) for i in idx[torch.from_numpy(conflict)].tolist()))
+    assert torch.equal(pool[shared], d["state"][shared]), "a conflicting slot was written"
+    assert_close(host(pool), pool_ref, STATE_RTOL, STATE_ATOL, "pool")
+
+
 @pytest.mark.parametrize("B", [1, 8])
 def test_decode_edge_gates(gpu, B):
     """The gate prologue's edge branches against the oracle: softplus arguments above 20,
@@ -212,6 +249,38 @@ def test_decode_every_launch_shape(gpu):
             ptr(d["a"]), ptr(d["dt_bias"]), ptr(d["b"]), d["scale"], ptr(out), 4, *H, variant, stream))
         torch.cuda.synchronize()
         assert_close(host(out), op_ref, OUT_RTOL, OUT_ATOL, f"shape {variant} pooled output")
+        assert_close(host(pool), pool_ref, STATE_RTOL, STATE_ATOL, f"shape {variant} pool")
+
+
+@pytest.mark.conflicts_expected
+def test_decode_pooled_duplicates_every_launch_shape(gpu):
+    """Every compiled launch shape on a pooled batch whose rows 0 and 3 share a slot:
+    both rows skipped (zero output, slot bit-identical), the others against the oracle,
+    and two conflicts counted per launch."""
+    lib = _lib.load()
+    stream = torch.cuda.current_stream(gpu).cuda_stream
+    ptr = lambda t: None if t is None else t.data_ptr()
+    slots = 11
+    wp = workloads.decode_inputs(5, seed=34, gate="slow", pool_slots=slots, state_scale=1.0)
+    idx = wp["state_indices"].clone()
+    idx[3] = idx[0]
+    op_ref, pool_ref = O.decode_pooled(*[to_numpy(wp[k]) for k in ("q", "k", "v", "state")],
+                                       idx.numpy(), *[to_numpy(wp[k]) for k in
+                                                      ("A_log", "a", "dt_bias", "b")], wp["scale"])
+    H = (16, 16, 32, 128, 128)
+    d = {k: (v.to(gpu) if isinstance(v, torch.Tensor) else v) for k, v in wp.items()}
+    binding.decode_pool_conflicts(reset=True)
+    for variant in range(lib.gdn_decode_num_variants()):
+        say(f"decode pooled duplicates, launch shape {variant}")
+        pool = d["state"].clone()
+        out = torch.full_like(d["v"], float("nan"))
+        _lib.check(lib.gdn_decode_pooled_with_variant(
+            ptr(d["q"]), ptr(d["k"]), ptr(d["v"]), ptr(pool), slots, ptr(idx.to(gpu)), ptr(d["A_log"]),
+            ptr(d["a"]), ptr(d["dt_bias"]), ptr(d["b"]), d["scale"], ptr(out), 5, *H, variant, stream))
+        assert binding.decode_pool_conflicts(reset=True) == 2, f"shape {variant}"
+        assert not host(out)[[0, 3]].any()
+        assert_close(host(out), op_ref, OUT_RTOL, OUT_ATOL, f"shape {variant} pooled output")
+        assert torch.equal(pool[int(idx[0])], d["state"][int(idx[0])])
         assert_close(host(pool), pool_ref, STATE_RTOL, STATE_ATOL, f"shape {variant} pool")
 
 

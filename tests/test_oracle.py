@@ -256,6 +256,28 @@ def test_decode_pooled_is_gather_decode_scatter():
     np.testing.assert_array_equal(new_pool[untouched], pool[untouched])
 
 
+def test_decode_pooled_conflicting_rows_are_padding():
+    """Rows that name a slot another in-range row also names are skipped like padding:
+    zero output, the slot keeps its bits; every other row is the plain decode of its
+    own slot, computed row by row here."""
+    c = decode_case(B=7, seed=12)
+    r = np.random.default_rng(12)
+    pool = r.standard_normal((8, 4, 16, 16))
+    idx = np.array([5, 2, 5, -3, 7, 2, 5])     # slot 5 three times, slot 2 twice, row 3 padding
+    conflict = O.pool_conflicts(idx, 8)
+    np.testing.assert_array_equal(conflict, [True, True, True, False, False, True, True])
+    o, new_pool = O.decode_pooled(c["q"], c["k"], c["v"], pool, idx, c["A_log"], c["a"],
+                                  c["dt_bias"], c["b"], None)
+    assert not o[[0, 1, 2, 3, 5, 6]].any()
+    o4, S4 = O.decode(c["q"][4:5], c["k"][4:5], c["v"][4:5], pool[7:8], c["A_log"], c["a"][4:5],
+                      c["dt_bias"], c["b"][4:5], None)
+    np.testing.assert_array_equal(o[4:5], o4)
+    np.testing.assert_array_equal(new_pool[7], S4[0])
+    untouched = [0, 1, 2, 3, 4, 5, 6]
+    np.testing.assert_array_equal(new_pool[untouched], pool[untouched])
+    assert not O.pool_conflicts(np.array([3, 9, -1, 9]), 8).any()  # out-of-range repeats are padding
+
+
 # --------------------------------------------------------------------------- prefill
 def test_prefill_T1_equals_decode():
     c = prefill_case([1], seed=1, gate="baseline", state_scale=0.05)

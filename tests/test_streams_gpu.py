@@ -1,11 +1,12 @@
 """Launches on several streams at once.  The kernels keep nothing between calls (the
-prefill hand-offs live in each workgroup's LDS; a workspace belongs to one call), so
-decode and prefill batches running concurrently on separate streams give the results
-of the same calls run one after another, bit for bit."""
+prefill hand-offs live in each workgroup's LDS; a workspace belongs to one call; the
+library's two scratch arrays are each ordered between launches by an event), so decode
+and prefill batches running concurrently on separate streams give the results of the
+same calls run one after another, bit for bit."""
 import pytest
 import torch
 
-from gdn_kernel_amd import binding, workloads
+from gdn_kernel_amd import _lib, binding, workloads
 from tests.gpu_util import say
 
 pytestmark = pytest.mark.gpu
@@ -17,15 +18,28 @@ def _outputs(p, N):
             torch.full((N, Hv, 128, 128), float("nan"), device=p["v"].device, dtype=torch.float32))
 
 
+def _no_alloc(p, o, st):
+    """gdn_prefill_no_alloc through the C ABI on the current stream."""
+    lib = _lib.load()
+    T, Hq, Hk, Hv = p["q"].shape[0], p["q"].shape[1], p["k"].shape[1], p["v"].shape[1]
+    N = p["cu_seqlens"].numel() - 1
+    ptr = lambda t: None if t is None else t.data_ptr()
+    _lib.check(lib.gdn_prefill_no_alloc(
+        ptr(p["q"]), ptr(p["k"]), ptr(p["v"]), ptr(p["state"]), ptr(p["A_log"]), ptr(p["a"]),
+        ptr(p["dt_bias"]), ptr(p["b"]), p["cu_seqlens"].data_ptr(), _lib.GDN_INDEX_INT32, N, T,
+        p["scale"], ptr(o), ptr(st), Hq, Hk, Hv, 128, 128, torch.cuda.current_stream().cuda_stream))
+
+
 def test_concurrent_streams_match_sequential(gpu):
-    """Six streams: decode B=64 out of place; prefill with 128 chains (split 2 ways);
+    """Eight streams: decode B=64 out of place; prefill with 128 chains (split 2 ways);
     prefill with 32 chains (split 8 ways); the same 32 chains with a workspace (prep
-    kernel + state pass); and two drop-in calls on one 3,000-token sequence, which run
-    the two-kernel path in the library's drop-in scratch (ordered between the streams by
-    the library).  Each stream launches its call three times with no synchronisation in
-    between."""
+    kernel + state pass); two drop-in calls on one 3,000-token sequence, which run the
+    two-kernel path in the library's drop-in scratch; and two gdn_prefill_no_alloc calls
+    on 2,000-token sequences, in the library's other scratch (each array ordered between
+    the streams by the library).  Each stream launches its call three times with no
+    synchronisation in between."""
     say("concurrent streams: decode B=64, prefill 128 chains, 32 chains, 32 chains with a workspace, "
-        "two 3,000-token drop-in calls")
+        "two 3,000-token drop-in calls, two 2,000-token no-alloc calls")
     w = workloads.decode_inputs(64, seed=51, device=gpu, gate="slow", state_scale=0.5)
     pa = workloads.prefill_inputs([700, 64, 5, 300], seed=52, device=gpu, gate="slow", state_scale=0.5)
     pb = workloads.prefill_inputs([900], seed=53, device=gpu, gate="slow", state_scale=0.5)
@@ -37,6 +51,10 @@ def test_concurrent_streams_match_sequential(gpu):
     c_o, c_s = _outputs(pb, 1)
     e_o, e_s = _outputs(pc, 1)
     f_o, f_s = _outputs(pd, 1)
+    pg = workloads.prefill_inputs([2000], seed=56, device=gpu, gate="slow", state_scale=0.5)
+    ph = workloads.prefill_inputs([2000], seed=57, device=gpu, gate="slow", state_scale=0.5)
+    g_o, g_s = _outputs(pg, 1)
+    h_o, h_s = _outputs(ph, 1)
     T, Hv = pb["v"].shape[0], pb["v"].shape[1]
     nbytes = binding.prefill_workspace_bytes(1, T, Hv)
     assert nbytes > 0, "the 32-chain batch is expected to take the two-kernel path"
@@ -54,8 +72,11 @@ def test_concurrent_streams_match_sequential(gpu):
         lambda: binding.prefill_kernel_with_workspace(*pre(pb, c_o, c_s), ws),
         lambda: binding.prefill_kernel(*pre(pc, e_o, e_s)),
         lambda: binding.prefill_kernel(*pre(pd, f_o, f_s)),
+        lambda: _no_alloc(pg, g_o, g_s),
+        lambda: _no_alloc(ph, h_o, h_s),
     ]
-    results = [(dec_o, dec_s), (a_o, a_s), (b_o, b_s), (c_o, c_s), (e_o, e_s), (f_o, f_s)]
+    results = [(dec_o, dec_s), (a_o, a_s), (b_o, b_s), (c_o, c_s), (e_o, e_s), (f_o, f_s),
+               (g_o, g_s), (h_o, h_s)]
 
     for call in calls:                          # one after another on the current stream
         call()
