@@ -253,6 +253,22 @@ __device__ __forceinline__ f32x4 mfma(const uint4& a, const uint4& b, f32x4 c) {
 
 __device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
 
+// Raw buffer resource over [base, base + bytes): a vector store whose byte offset
+// (plus its size) reaches past `bytes` is dropped by the hardware, which replaces a
+// per-lane branch around stores that may fall outside a chunk.  The third dword is
+// the gfx9 raw-buffer format word (32-bit data format, no swizzle, no stride).
+typedef __amdgpu_buffer_rsrc_t BufferRsrc;
+typedef uint32_t u32x2 __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ BufferRsrc buffer_rsrc(void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(base, short(0), int(bytes), 0x00020000);
+}
+__device__ __forceinline__ void buffer_store16(u32x4 v, BufferRsrc r, int offset) {
+  __builtin_amdgcn_raw_buffer_store_b128(v, r, offset, 0, 0);
+}
+__device__ __forceinline__ void buffer_store8(u32x2 v, BufferRsrc r, int offset) {
+  __builtin_amdgcn_raw_buffer_store_b64(v, r, offset, 0, 0);
+}
+
 // Calls f(std::integral_constant<int, I>) for I = 0 .. N-1 (compile-time indices).
 template <int I, int N, class Fn>
 __device__ __forceinline__ void static_for_impl(Fn&& f) {
@@ -1769,24 +1785,6 @@ __device__ __forceinline__ void consumer_loop(PrefillSmem& sm, const PrefillArgs
         for (int vt = 0; vt < VT; ++vt) Xq[vt][ct] = mfma(vb[vt], pq, Xq[vt][ct]);
       }
     }
-    // Lane holds o[c = 16ct + n16][v = row0 + VW w + vrow(vt, 4g + i)]: with two tiles
-    // that is 8 consecutive v (one 16-byte store per ct), with one 4 (8 bytes).
-    uint16_t* obase = p.out + cs * vstride + (int64_t(h) * D + row0 + VW * wave);
-#pragma unroll
-    for (int ct = 0; ct < 4; ++ct) {
-      if (16 * ct + n16 < clen) {
-        if constexpr (VT == 2) {
-          const f32x4 &o0 = Xq[0][ct], &o1 = Xq[1][ct];
-          *reinterpret_cast<uint4*>(obase + orow[ct]) =
-              uint4{pack_bf16x2(o0[0], o0[1]), pack_bf16x2(o0[2], o0[3]), pack_bf16x2(o1[0], o1[1]),
-                    pack_bf16x2(o1[2], o1[3])};
-        } else {
-          const f32x4& o = Xq[0][ct];
-          *reinterpret_cast<uint2*>(obase + orow[ct]) = uint2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])};
-        }
-      }
-    }
-
     clk.lap(4);
     // 3: S = e^{gamma_last} S + sum_c K[c]^T (d_c v_new[c]),  d_c = e^{gamma_last - gamma_c}
     const float dlast = cb.eg[clen - 1];
@@ -1814,6 +1812,28 @@ __device__ __forceinline__ void consumer_loop(PrefillSmem& sm, const PrefillArgs
         }
       });
     });
+    // The output stores, in the same block as the state update so that their packing
+    // and issue fill the update's MFMA shadow.  Lane holds o[c = 16ct + n16][v = row0 +
+    // VW w + vrow(vt, 4g + i)]: with two tiles 8 consecutive v (one 16-byte store per
+    // ct), with one 4 (8 bytes).  Rows at or past clen fall outside the buffer
+    // resource, whose extent ends at the chunk's last token: the hardware drops their
+    // stores, so no lane needs a branch.
+    {
+      const BufferRsrc orsrc = buffer_rsrc(p.out + cs * vstride + (int64_t(h) * D + row0 + VW * wave),
+                                           uint32_t(clen) * uint32_t(vstride) * 2u);
+#pragma unroll
+      for (int ct = 0; ct < 4; ++ct) {
+        if constexpr (VT == 2) {
+          const f32x4 &o0 = Xq[0][ct], &o1 = Xq[1][ct];
+          buffer_store16(u32x4{pack_bf16x2(o0[0], o0[1]), pack_bf16x2(o0[2], o0[3]), pack_bf16x2(o1[0], o1[1]),
+                               pack_bf16x2(o1[2], o1[3])},
+                         orsrc, 2 * orow[ct]);
+        } else {
+          const f32x4& o = Xq[0][ct];
+          buffer_store8(u32x2{pack_bf16x2(o[0], o[1]), pack_bf16x2(o[2], o[3])}, orsrc, 2 * orow[ct]);
+        }
+      }
+    }
     signal_count(sm, kConsumed, lane);  // buffers of this chunk no longer read
     clk.lap(5);
   }
