@@ -81,9 +81,12 @@ def test_decode_empty_batch(gpu):
 
 
 @pytest.mark.parametrize("gate", ["baseline", "slow"])
-def test_decode_pooled_matches_oracle(gpu, gate):
-    say(f"decode pooled small gate={gate}")
-    slots, B = 40, 12
+@pytest.mark.parametrize("B", [12, 8])
+def test_decode_pooled_matches_oracle(gpu, gate, B):
+    """Pooled decode with padding rows against the oracle: B = 12 over 40 slots runs
+    slot-major (at most 4 slots per row), B = 8 row-major."""
+    say(f"decode pooled small gate={gate} B={B}")
+    slots = 40
     w = workloads.decode_inputs(B, seed=9, gate=gate, pool_slots=slots,
                                 state_scale=1.0 if gate == "slow" else 0.05)
     idx = w["state_indices"].clone()
@@ -104,6 +107,30 @@ def test_decode_pooled_matches_oracle(gpu, gate):
     used = set(int(i) for i in idx.tolist() if 0 <= i < slots)
     untouched = [s for s in range(slots) if s not in used]
     assert torch.equal(pool[untouched], d["state"][untouched]), "untouched slots changed"
+
+
+def test_decode_pooled_more_rows_than_slots(gpu):
+    """24 rows over 10 slots (slot-major): rows 0-9 name every slot once, rows 10-23 are
+    padding (negative or past the pool), written by the grid's padding workgroups."""
+    say("decode pooled: 24 rows over 10 slots")
+    slots, B = 10, 24
+    w = workloads.decode_inputs(B, seed=77, gate="slow", pool_slots=24, state_scale=1.0)
+    pool0 = w["state"][:slots].clone()
+    idx = torch.cat([torch.randperm(slots, generator=torch.Generator().manual_seed(5)).to(torch.int32),
+                     torch.tensor([-1, 10, 11, -7, 40, 12, -1, 99, 10, 13, -2, 1000, 15, -3],
+                                  dtype=torch.int32)])
+    o_ref, pool_ref = O.decode_pooled(*[to_numpy(w[k]) for k in ("q", "k", "v")], to_numpy(pool0),
+                                      idx.numpy(), *[to_numpy(w[k]) for k in
+                                                     ("A_log", "a", "dt_bias", "b")], w["scale"])
+    d = {k: (v.to(gpu) if isinstance(v, torch.Tensor) else v) for k, v in w.items()}
+    pool = pool0.to(gpu)
+    out = torch.full_like(d["v"], float("nan"))
+    binding.decode_pooled_kernel(d["q"], d["k"], d["v"], pool, d["A_log"], d["a"], d["dt_bias"],
+                                 d["b"], d["scale"], out, idx.to(gpu))
+    torch.cuda.synchronize()
+    assert not host(out)[10:].any()
+    assert_close(host(out), o_ref, OUT_RTOL, OUT_ATOL, "output")
+    assert_close(host(pool), pool_ref, STATE_RTOL, STATE_ATOL, "pool")
 
 
 def test_decode_pooled_config2_full_size(gpu):
@@ -137,14 +164,16 @@ def test_decode_pooled_config2_full_size(gpu):
 
 
 @pytest.mark.conflicts_expected
-@pytest.mark.parametrize("heads,B,slots", [((16, 16, 32), 12, 40), ((1, 1, 4), 20, 64),
-                                           ((1, 1, 4), 1500, 2048)])
+@pytest.mark.parametrize("heads,B,slots", [((16, 16, 32), 12, 40), ((16, 16, 32), 8, 40),
+                                           ((1, 1, 4), 20, 64), ((1, 1, 4), 1500, 2048),
+                                           ((1, 1, 4), 1500, 8000)])
 def test_decode_pooled_duplicate_slots(gpu, heads, B, slots):
     """Rows naming a slot that another row also names: a pair at the first and last row
     (the two ends of the index scan), a triple in the middle, plus a padding row.  Each
     conflicting row has zero output and its slot keeps its bits; every other row matches
     the oracle; gdn_decode_pool_conflicts counts the five skipped rows.  The layouts take
-    one-wave (B*Hv < 128) and four-wave workgroups, the last over several scan passes."""
+    one-wave (B*Hv < 128) and four-wave workgroups, over several scan passes for B = 1500,
+    slot-major (at most 4 slots per row) and row-major (8 over 40, 1500 over 8000)."""
     say(f"decode pooled duplicate slots heads={heads} B={B} slots={slots}")
     w = workloads.decode_inputs(B, Heads(*heads), seed=40 + B, gate="slow", pool_slots=slots,
                                 state_scale=1.0)
@@ -253,14 +282,14 @@ def test_decode_every_launch_shape(gpu):
 
 
 @pytest.mark.conflicts_expected
-def test_decode_pooled_duplicates_every_launch_shape(gpu):
-    """Every compiled launch shape on a pooled batch whose rows 0 and 3 share a slot:
-    both rows skipped (zero output, slot bit-identical), the others against the oracle,
-    and two conflicts counted per launch."""
+@pytest.mark.parametrize("slots", [11, 30])
+def test_decode_pooled_duplicates_every_launch_shape(gpu, slots):
+    """Every compiled launch shape on a pooled batch of 5 rows whose rows 0 and 3 share a
+    slot: both rows skipped (zero output, slot bit-identical), the others against the
+    oracle, and two conflicts counted per launch; 11 slots run slot-major, 30 row-major."""
     lib = _lib.load()
     stream = torch.cuda.current_stream(gpu).cuda_stream
     ptr = lambda t: None if t is None else t.data_ptr()
-    slots = 11
     wp = workloads.decode_inputs(5, seed=34, gate="slow", pool_slots=slots, state_scale=1.0)
     idx = wp["state_indices"].clone()
     idx[3] = idx[0]
@@ -271,7 +300,7 @@ def test_decode_pooled_duplicates_every_launch_shape(gpu):
     d = {k: (v.to(gpu) if isinstance(v, torch.Tensor) else v) for k, v in wp.items()}
     binding.decode_pool_conflicts(reset=True)
     for variant in range(lib.gdn_decode_num_variants()):
-        say(f"decode pooled duplicates, launch shape {variant}")
+        say(f"decode pooled duplicates, {slots} slots, launch shape {variant}")
         pool = d["state"].clone()
         out = torch.full_like(d["v"], float("nan"))
         _lib.check(lib.gdn_decode_pooled_with_variant(
