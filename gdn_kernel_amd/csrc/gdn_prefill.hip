@@ -539,46 +539,6 @@ __device__ __forceinline__ bool aborted(Smem& sm) {
 
 constexpr uint32_t kNaNx2 = 0x7fc07fc0u;  // two bf16 quiet NaNs
 
-#ifdef GDN_PREFILL_PHASE_CLOCKS
-// Development builds only (-DGDN_PREFILL_PHASE_CLOCKS): core-clock cycles that
-// each wave spends in each phase of its chunk loop, summed over its chunks, for
-// the first kClockWGs workgroups of a launch (read back with
-// gdn_prefill_phase_clocks_read).  Every lap is an s_memtime, whose wait also
-// drains the wave's outstanding LDS operations, so phases are slightly longer
-// than in the default build.
-}  // namespace
-constexpr int kClockPhases = 12, kClockWGs = 2048;
-__device__ uint32_t gdn_prefill_phase_clocks[kClockWGs * 8 * kClockPhases];
-namespace {
-struct PhaseClock {
-  uint64_t last;
-  uint32_t acc[kClockPhases];
-  __device__ __forceinline__ void start() {
-#pragma unroll
-    for (int i = 0; i < kClockPhases; ++i) acc[i] = 0;
-    last = __builtin_amdgcn_s_memtime();
-  }
-  __device__ __forceinline__ void lap(int ph) {
-    const uint64_t t = __builtin_amdgcn_s_memtime();
-    acc[ph] += uint32_t(t - last);
-    last = t;
-  }
-  __device__ __forceinline__ void store(int wave, int lane) {
-    if (blockIdx.x < unsigned(kClockWGs) && lane < kClockPhases) {
-      uint32_t v = 0;
-#pragma unroll
-      for (int i = 0; i < kClockPhases; ++i) v = lane == i ? acc[i] : v;
-      gdn_prefill_phase_clocks[(blockIdx.x * 8 + wave) * kClockPhases + lane] = v;
-    }
-  }
-};
-#else
-struct PhaseClock {
-  __device__ __forceinline__ void start() {}
-  __device__ __forceinline__ void lap(int) {}
-  __device__ __forceinline__ void store(int, int) {}
-};
-#endif
 
 // The parity-selected LDS buffers of one chunk.
 struct ChunkBufs {
@@ -1056,8 +1016,6 @@ __device__ __forceinline__ void producer_loop(Smem& sm, const PrefillArgs& p, in
   // of tick t, where it has slack) and stores them with the chunk's K and Q.
   ChunkGates gts = {0.f, 0.f, 0.f, 0.f, 0.f};
   if (pw == 0) gts = chunk_gates(f, lane0, int(s1 - s0 < C ? s1 - s0 : C), neg_decay, dt_bias);
-  PhaseClock clk;
-  clk.start();
 
   int u = 0;
   for (;;) {
@@ -1096,7 +1054,6 @@ __device__ __forceinline__ void producer_loop(Smem& sm, const PrefillArgs& p, in
         copy_tiles_out<Smem>(chunk_bufs(sm, (t - 1) & 1), images + int64_t(t - 1) * p.Hv * kTileImage, pt, aborted(sm));
       }
     }
-    clk.lap(0);
 
     // 1: stage K/Q (permuted columns), gates
     stage_kq(cb, f, pt);
@@ -1111,10 +1068,8 @@ __device__ __forceinline__ void producer_loop(Smem& sm, const PrefillArgs& p, in
         if (vrow[it] < clen) fv[it] = *reinterpret_cast<const uint4*>(vb + voff[it]);
       }
     }
-    clk.lap(1);
     signal_count(sm, kPPhase, lane);
     wait_count<V::kHooks>(sm, kPPhase, 4 * (2 * u + 1));  // all of K/Q/gates staged
-    clk.lap(2);
     // The rest of the chunk is the longer chain: producer waves go ahead of the
     // consumer wave sharing the SIMD.
     __builtin_amdgcn_s_setprio(1);
@@ -1128,16 +1083,12 @@ __device__ __forceinline__ void producer_loop(Smem& sm, const PrefillArgs& p, in
     // after its solve.
     constexpr bool kSolveFirst = V::F > 1;
     if (!kSolveFirst && has_next) producer_prefetch(p, ncs, nclen, h, hq, hk, pt, lo, f);
-    clk.lap(10);
     switch (pw) {
       case 0:
         diag_tiles<0, 1>(sm, cb, lane);
         signal_count(sm, kDiagN, lane);
-        clk.lap(3);
         wait_count<V::kHooks>(sm, kDiagN, 4 * (u + 1));
-        clk.lap(4);
         diag_solve(sm, cb, lane);
-        clk.lap(5);
         break;
       case 1: {
         diag_tiles<1, 2>(sm, cb, lane);
@@ -1170,10 +1121,8 @@ __device__ __forceinline__ void producer_loop(Smem& sm, const PrefillArgs& p, in
         break;
       }
     }
-    clk.lap(3);
     signal_count(sm, kPPhase, lane);
     wait_count<V::kHooks>(sm, kPPhase, 4 * (2 * u + 2));  // diagonal blocks and N tiles done
-    clk.lap(6);
 
     // 3: off-diagonal blocks of T~ (waves 1 and 3), the remaining P tiles (two
     // each on waves 0 and 2), V once the consumers have read the previous chunk's
@@ -1198,9 +1147,7 @@ __device__ __forceinline__ void producer_loop(Smem& sm, const PrefillArgs& p, in
         offdiag_left<V::kHooks>(sm, cb, u, lane);
         break;
     }
-    clk.lap(7);
     if (u >= 1) wait_count<V::kHooks>(sm, kVFree, V::NCW * u);
-    clk.lap(8);
 #pragma unroll
     for (int it = 0; it < NVIT; ++it) {
       const int seg = pt + it * NPROD;
@@ -1209,7 +1156,6 @@ __device__ __forceinline__ void producer_loop(Smem& sm, const PrefillArgs& p, in
     }
     __builtin_amdgcn_s_setprio(0);
     if (!V::kHooks || p.ready_chunks <= 0 || t < p.ready_chunks) signal_count(sm, kReady, lane);
-    clk.lap(9);
   }
   if constexpr (!V::kPersist) {
     break;
@@ -1226,7 +1172,6 @@ __device__ __forceinline__ void producer_loop(Smem& sm, const PrefillArgs& p, in
     copy_tiles_out<Smem>(chunk_bufs(sm, (nchunks - 1) & 1), images + int64_t(nchunks - 1) * p.Hv * kTileImage, pt,
                    aborted(sm));
   }
-  clk.store(V::NCW + pw, lane0);
 }
 
 // The raw gate inputs (a, b) of token `lane` of a chunk, clamped into the chunk.
@@ -1327,8 +1272,6 @@ __device__ __forceinline__ void producer_loop_split(PrefillSmem& sm, const Prefi
 
   ProducerPrefetchT<NST> f = {};
   uint4 fv[NVIT];
-  PhaseClock clk;
-  clk.start();
   // Chunk 0 ahead of the loop: its gates, K/Q, and diagonal N tiles.
   if (pw == 0) {
     prefetch_gate_inputs(p, s0, chunk_len(s0), h, lane0, f);
@@ -1350,7 +1293,6 @@ __device__ __forceinline__ void producer_loop_split(PrefillSmem& sm, const Prefi
     diag_tile(chunk_bufs(sm, 0), lane0);
     signal_count(sm, kDiagN, lane0);
   }
-  clk.lap(0);
 
   for (int t = 0; t < nchunks; ++t) {
     int lane = lane0;
@@ -1362,15 +1304,12 @@ __device__ __forceinline__ void producer_loop_split(PrefillSmem& sm, const Prefi
     switch (pw) {
       case 0:
         wait_count<V::kHooks>(sm, kDiagN, 4 * (t + 1));
-        clk.lap(1);
         diag_solve(sm, cb, lane);
         signal_count(sm, kPPhase, lane);
-        clk.lap(2);
         if (ncs < s1) {
           // Chunk t + 1's gates, stored into the buffers of chunk t - 1 once consumed.
           const ChunkGates g = chunk_gates(f, lane, chunk_len(ncs), neg_decay, dt_bias);
           if (t >= 1) wait_count<V::kHooks>(sm, kConsumed, V::NCW * t);
-          clk.lap(3);
           const ChunkBufs cbn = chunk_bufs(sm, (t + 1) & 1);
           store_gates(cbn, g, lane);
           signal_count(sm, kStaged, lane);
@@ -1383,39 +1322,30 @@ __device__ __forceinline__ void producer_loop_split(PrefillSmem& sm, const Prefi
             signal_count(sm, kDiagN, lane);
           }
         }
-        clk.lap(4);
         break;
       case 1: {
         wait_count<V::kHooks>(sm, kStaged, (NS + 1) * (t + 1));
         if (t >= 1) wait_count<V::kHooks>(sm, kNRead, t);  // chunk t - 1's N read by the left wave
-        clk.lap(1);
         const TileJob j1[2] = {{1, 2, 1}, {1, 3, 2}};
         run_tiles(sm, cb, j1, p.scale, lane);
         const TileJob j2[2] = {{1, 3, 1}, {2, 3, 3}};
         run_tiles(sm, cb, j2, p.scale, lane);
         signal_count(sm, kPPhase, lane);
-        clk.lap(2);
         wait_count<V::kHooks>(sm, kPPhase, 3 * (t + 1));
-        clk.lap(3);
         offdiag_right(sm, cb, t, lane);
         ready(t, lane);
-        clk.lap(4);
         break;
       }
       case 3: {
         wait_count<V::kHooks>(sm, kStaged, (NS + 1) * (t + 1));
-        clk.lap(1);
         const TileJob j1[2] = {{1, 1, 0}, {1, 2, 0}};
         run_tiles(sm, cb, j1, p.scale, lane);
         const TileJob j2[2] = {{1, 3, 0}, {2, 2, 2}};
         run_tiles(sm, cb, j2, p.scale, lane);
         signal_count(sm, kPPhase, lane);
-        clk.lap(2);
         wait_count<V::kHooks>(sm, kPPhase, 3 * (t + 1));
-        clk.lap(3);
         offdiag_left<V::kHooks, true>(sm, cb, t, lane);
         ready(t, lane);
-        clk.lap(4);
         break;
       }
       default: {  // stagers
@@ -1431,32 +1361,26 @@ __device__ __forceinline__ void producer_loop_split(PrefillSmem& sm, const Prefi
         signal_count(sm, kVStaged, lane);
         if (ncs < s1) load_v(fv, ncs);  // chunk t + 1's V into registers
         wait_count<V::kHooks>(sm, kStaged, (NS + 1) * (t + 1));  // chunk t's gates (wave 0)
-        clk.lap(1);
         stager_tiles(cb, lane);
         ready(t, lane);  // chunk t's P tiles
-        clk.lap(2);
         if (ncs < s1) {
           // Chunk t + 1: K and Q into the buffers of chunk t - 1 once consumed; its
           // diagonal N tiles once the solve of chunk t freed their scratch.
           if (t >= 1) wait_count<V::kHooks>(sm, kConsumed, V::NCW * t);
-          clk.lap(3);
           const ChunkBufs cbn = chunk_bufs(sm, (t + 1) & 1);
           stage_kq(cbn, f, pt);
           signal_count(sm, kStaged, lane);
           if (ncs + C < s1) producer_prefetch(p, ncs + C, chunk_len(ncs + C), h, hq, hk, pt, lo, f);
           wait_count<V::kHooks>(sm, kStaged, (NS + 1) * (t + 2));
           wait_count<V::kHooks>(sm, kPPhase, 3 * (t + 1));
-          clk.lap(5);
           diag_tile(cbn, lane);
           signal_count(sm, kDiagN, lane);
         }
-        clk.lap(4);
         break;
       }
     }
     __builtin_amdgcn_s_setprio(0);
   }
-  clk.store(V::NCW + pw, lane0);
 }
 
 // The loader loop of the two-kernel path: the producers' hand-offs and staging,
@@ -1513,8 +1437,6 @@ __device__ __forceinline__ void loader_loop(PrefillSmem& sm, const PrefillArgs& 
       if (vrow[it] < clen0) fv[it] = *reinterpret_cast<const u32x4*>(vb + voff[it]);
     }
   }
-  PhaseClock clk;
-  clk.start();
 
   auto tick = [&](int t, u32x4(&tv)[NTIT]) {
     int lane = lane0;
@@ -1524,10 +1446,8 @@ __device__ __forceinline__ void loader_loop(PrefillSmem& sm, const PrefillArgs& 
     const int nclen = int(s1 - ncs < C ? s1 - ncs : C);
     const ChunkBufs cb = chunk_bufs(sm, t & 1);
     if (t >= 2) wait_count<V::kHooks>(sm, kConsumed, V::NCW * (t - 1));  // chunk t - 2 consumed
-    clk.lap(0);
     stage_kq(cb, f, pt);
     if (ncs < s1) producer_prefetch(p, ncs, nclen, h, hq, hk, pt, lo, f);
-    clk.lap(1);
 #pragma unroll
     for (int it = 0; it < NTIT; ++it) {
       const int e = pt + it * NPROD;
@@ -1543,9 +1463,7 @@ __device__ __forceinline__ void loader_loop(PrefillSmem& sm, const PrefillArgs& 
 #pragma unroll
       for (int it = 0; it < NTIT; ++it) tv[it] = src[toff[it]];
     }
-    clk.lap(7);
     if (t >= 1) wait_count<V::kHooks>(sm, kVFree, V::NCW * t);  // the consumers' last read of V
-    clk.lap(8);
 #pragma unroll
     for (int it = 0; it < NVIT; ++it) {
       const int seg = pt + it * NPROD;
@@ -1566,7 +1484,6 @@ __device__ __forceinline__ void loader_loop(PrefillSmem& sm, const PrefillArgs& 
         if (vrow[it] < nclen) fv[it] = *reinterpret_cast<const u32x4*>(vb + voff[it]);
       }
     }
-    clk.lap(9);
   };
   if constexpr (deep) {
     for (int t = 0; t < nchunks; t += 2) {
@@ -1576,7 +1493,6 @@ __device__ __forceinline__ void loader_loop(PrefillSmem& sm, const PrefillArgs& 
   } else {
     for (int t = 0; t < nchunks; ++t) tick(t, tva);
   }
-  clk.store(V::NCW + pw, lane0);
 }
 
 // ---------------------------------------------------------------------------
@@ -1666,8 +1582,6 @@ __device__ __forceinline__ void consumer_loop(PrefillSmem& sm, const PrefillArgs
   int orow[4];
 #pragma unroll
   for (int ct = 0; ct < 4; ++ct) orow[ct] = (16 * ct + (lane0 & 15)) * int(vstride) + (VT == 2 ? 8 : 4) * (lane0 >> 4);
-  PhaseClock clk;
-  clk.start();
   for (int t = 1; t <= nchunks; ++t) {
     int lane = lane0;
     asm volatile("" : "+v"(lane));
@@ -1686,12 +1600,10 @@ __device__ __forceinline__ void consumer_loop(PrefillSmem& sm, const PrefillArgs
     } else {
       wait_count<V::kHooks>(sm, kReady, 4 * u);  // chunk u - 1 prepared
     }
-    clk.lap(0);
 
     // 1: X = K S^T, (Q S^T)^T
     f32x4 Xk[4][VT], Xq[VT][4];
     retrieve(cb, S, Xk, Xq, lane);
-    clk.lap(1);
 
     // 2: Y, v_new, output
     // Y = beta (V - e^gamma X); element (c = 16ct + 4g + i, v = VW w + vrow(vt, n16)).
@@ -1715,7 +1627,6 @@ __device__ __forceinline__ void consumer_loop(PrefillSmem& sm, const PrefillArgs
     }
     signal_count(sm, kVFree, lane);  // V of this chunk read
     if constexpr (V::kPipelined) wait_count<V::kHooks>(sm, kReady, (V::kStagers + 2) * u);  // T~ and P
-    clk.lap(2);
     // The 16-row consumer reads all its T~ and P operands now (they are ready), so that
     // their latency overlaps the Y split; the 32-row one, short of registers, as used.
     // Pair (ct, js) of T~ is fragment ct < 2 ? ct : 2 ct - 2 + js; pair (js, ct) of
@@ -1766,7 +1677,6 @@ __device__ __forceinline__ void consumer_loop(PrefillSmem& sm, const PrefillArgs
         }
       }
     }
-    clk.lap(3);
     // o^T = scale e^gamma (S Q^T) + v_new^T (scale P)^T (rows v, cols c); P is lower triangular.
 #pragma unroll
     for (int js = 0; js < 2; ++js) {
@@ -1785,7 +1695,6 @@ __device__ __forceinline__ void consumer_loop(PrefillSmem& sm, const PrefillArgs
         for (int vt = 0; vt < VT; ++vt) Xq[vt][ct] = mfma(vb[vt], pq, Xq[vt][ct]);
       }
     }
-    clk.lap(4);
     // 3: S = e^{gamma_last} S + sum_c K[c]^T (d_c v_new[c]),  d_c = e^{gamma_last - gamma_c}
     const float dlast = cb.eg[clen - 1];
     uint4 Uh[VT][2], Ul[VT][2];
@@ -1835,9 +1744,7 @@ __device__ __forceinline__ void consumer_loop(PrefillSmem& sm, const PrefillArgs
       }
     }
     signal_count(sm, kConsumed, lane);  // buffers of this chunk no longer read
-    clk.lap(5);
   }
-  clk.store(wave, lane0);
 }
 
 // The token-split consumer loop of the two-kernel state pass (F = 8).  The four
@@ -1877,8 +1784,6 @@ __device__ __forceinline__ void consumer_loop_tsplit(PrefillSmem& sm, const Pref
     sx[(2 * ct + 1) * 64 + lane0] = Sl;
     signal_count(sm, kSx, lane0);
   }
-  PhaseClock clk;
-  clk.start();
   for (int t = 1; t <= nchunks; ++t) {
     int lane = lane0;
     asm volatile("" : "+v"(lane));
@@ -1900,7 +1805,6 @@ __device__ __forceinline__ void consumer_loop_tsplit(PrefillSmem& sm, const Pref
       Sh[ks] = sx[(2 * ks) * 64 + lane];
       Sl[ks] = sx[(2 * ks + 1) * 64 + lane];
     }
-    clk.lap(0);
 
     // 1: block ct of X = K S^T and of (Q S^T)^T.
     f32x4 xk = zero4(), xq = zero4();
@@ -1910,7 +1814,6 @@ __device__ __forceinline__ void consumer_loop_tsplit(PrefillSmem& sm, const Pref
       xk = mfma(kf[ks], Sl[ks], xk);
       xq = mfma(Sh[ks], qf[ks], xq);
     }
-    clk.lap(1);
 
     // 2: Y for rows c = 16ct + 4g + i, as consumer_loop; the output block scaled.
     {
@@ -1942,7 +1845,6 @@ __device__ __forceinline__ void consumer_loop_tsplit(PrefillSmem& sm, const Pref
     f32x4 Y[4];
 #pragma unroll
     for (int c = 0; c < 4; ++c) Y[c] = yx[64 * c + lane];
-    clk.lap(2);
 
     // v_new = T~ Y, all 64 rows.
     uint4 Yh[2], Yl[2];
@@ -1960,7 +1862,6 @@ __device__ __forceinline__ void consumer_loop_tsplit(PrefillSmem& sm, const Pref
         Vn[c] = mfma(tl, Yh[js], Vn[c]);
       }
     }
-    clk.lap(3);
 
     // 3: columns 32ct .. 32ct + 31 of S = e^{gamma_last} S + sum_c K[c]^T (d_c v_new[c]).
     const float dlast = cb.eg[clen - 1];
@@ -1992,7 +1893,6 @@ __device__ __forceinline__ void consumer_loop_tsplit(PrefillSmem& sm, const Pref
       sx[(2 * ct + 1) * 64 + lane] = l2;
       signal_count(sm, kSx, lane);
     }
-    clk.lap(5);
 
     // Output block ct: o^T = scale e^gamma (S Q^T) + v_new^T (scale P)^T.
     xq = mfma(pack_hi(Vn[0], Vn[1]), pq0, xq);
@@ -2000,9 +1900,7 @@ __device__ __forceinline__ void consumer_loop_tsplit(PrefillSmem& sm, const Pref
     if (16 * ct + n16 < clen)
       *reinterpret_cast<uint2*>(p.out + cs * vstride + (int64_t(h) * D + row0) + orow) =
           uint2{pack_bf16x2(xq[0], xq[1]), pack_bf16x2(xq[2], xq[3])};
-    clk.lap(4);
   }
-  clk.store(wave, lane0);
 }
 
 // The sequence of rank `rank` in descending length order (ties: lower index
@@ -2779,12 +2677,3 @@ hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream, hipEvent_t d
 
 }  // namespace gdn
 
-#ifdef GDN_PREFILL_PHASE_CLOCKS
-// Copies the phase clocks of the last launch ([kClockWGs][8][kClockPhases]
-// uint32) to host memory; development builds only.
-extern "C" int gdn_prefill_phase_clocks_read(uint32_t* host, int64_t count) {
-  const int64_t n = count < int64_t(gdn::kClockWGs) * 8 * gdn::kClockPhases
-                        ? count : int64_t(gdn::kClockWGs) * 8 * gdn::kClockPhases;
-  return hipMemcpyFromSymbol(host, HIP_SYMBOL(gdn::gdn_prefill_phase_clocks), size_t(n) * 4) == hipSuccess ? 0 : 3;
-}
-#endif
