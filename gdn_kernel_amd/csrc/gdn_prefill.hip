@@ -532,6 +532,22 @@ __device__ __forceinline__ void wait_count(Smem& sm, int which, int target) {
   __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
 }
 
+// wait_count for counter `a`, reading counter `b` in the same LDS round trip:
+// returns whether `b` had reached `tb` then, so that a later wait for it can be
+// skipped (the acquire that ends this wait covers both).
+template <bool kHooks, class Smem>
+__device__ __forceinline__ bool wait_count_peek(Smem& sm, int a, int ta, int b, int tb) {
+  const int va = __hip_atomic_load(&sm.sync[a], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  const int vb = __hip_atomic_load(&sm.sync[b], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  const bool b_ok = __builtin_amdgcn_readfirstlane(int(vb >= tb)) != 0;
+  if (__builtin_amdgcn_readfirstlane(int(va >= ta)) != 0) {
+    __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "workgroup");
+  } else {
+    wait_count<kHooks>(sm, a, ta);
+  }
+  return b_ok;
+}
+
 template <class Smem>
 __device__ __forceinline__ bool aborted(Smem& sm) {
   return __hip_atomic_load(&sm.sync[kAbort], __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP) != 0;
@@ -1791,14 +1807,15 @@ __device__ __forceinline__ void consumer_loop_tsplit(PrefillSmem& sm, const Pref
     const int64_t cs = s0 + int64_t(t - 1) * C;
     const int clen = int(s1 - cs < C ? s1 - cs : C);
     const ChunkBufs cb = chunk_bufs(sm, (t - 1) & 1);
-    wait_count<V::kHooks>(sm, kReady, 4 * t);  // chunk t - 1 loaded
+    // Chunk t - 1 loaded; the state after chunk t - 2 looked at in the same read.
+    const bool sx_ready = wait_count_peek<V::kHooks>(sm, kReady, 4 * t, kSx, 4 * t);
     uint4 kf[4], qf[4];
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
       kf[ks] = frag_kq(cb.K, 16 * ct, ks, lane);
       qf[ks] = frag_kq(cb.Q, 16 * ct, ks, lane);
     }
-    wait_count<V::kHooks>(sm, kSx, 4 * t);  // the state after chunk t - 2
+    if (!sx_ready) wait_count<V::kHooks>(sm, kSx, 4 * t);  // the state after chunk t - 2
     uint4 Sh[4], Sl[4];
 #pragma unroll
     for (int ks = 0; ks < 4; ++ks) {
