@@ -84,66 +84,15 @@ __device__ __forceinline__ bool slot_named_elsewhere(const int32_t* slots, int B
   }
 }
 
-// The rows of the batch's B slot indices that name `slot`: their number, and one of
-// them (-1 if none).  The WAVES waves of a workgroup each scan an interleaved share,
-// four 64-index blocks per pass, and sum their counts through LDS.  Ends with a
-// workgroup barrier when WAVES > 1.
-template <int WAVES>
-__device__ __forceinline__ void slot_rows(const int32_t* slots, int B, int slot, int lane, int wave, int& count,
-                                          int& row) {
-  constexpr int STEP = 64 * WAVES;
-  int cnt = 0, r = -1;
-  for (int i0 = 64 * wave; i0 < B; i0 += 4 * STEP) {
-    int s[4];
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int i = i0 + u * STEP + lane;
-      s[u] = i < B ? slots[i] : -1;
-    }
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const uint64_t m = __builtin_amdgcn_ballot_w64(s[u] == slot);
-      cnt += __builtin_popcountll(m);
-      if (m != 0) r = i0 + u * STEP + __builtin_ctzll(m);
-    }
-  }
-  if constexpr (WAVES == 1) {
-    count = cnt;
-    row = r;
-  } else {
-    __shared__ int wave_count[WAVES], wave_row[WAVES];
-    if (lane == 0) {
-      wave_count[wave] = cnt;
-      wave_row[wave] = r;
-    }
-    __syncthreads();
-    count = 0;
-    row = -1;
-#pragma unroll
-    for (int w = 0; w < WAVES; ++w) {
-      count += wave_count[w];
-      if (wave_count[w] != 0) row = wave_row[w];
-    }
-  }
-}
-
 // RPW rows per wave, WAVES waves per workgroup; a workgroup covers RPW*WAVES
 // rows of one head and 128 / (RPW*WAVES) workgroups cover one head.
-//
-// Pooled launches run in one of two orders.  Row-major (SLOTMAJOR false): unit u of
-// the grid is batch row u, which reads its slot from the index vector.  Slot-major:
-// unit u < pool_slots is pool slot u, which finds the row naming it while it scans the
-// indices, so the state blocks are visited in ascending address order whatever the
-// order of the indices; the last B workgroups of the grid then write the zero outputs
-// of padding rows, which name no slot.
-template <int RPW, int WAVES, bool HAS_STATE, bool POOLED, bool NT, bool SLOTMAJOR = false>
+template <int RPW, int WAVES, bool HAS_STATE, bool POOLED, bool NT>
 __global__ __launch_bounds__(64 * WAVES) void gdn_decode_kernel(DecodeArgs p) {
   constexpr int D = kHeadDim;
   constexpr int NL = RPW / 2;
   constexpr int ROWS_PER_WG = RPW * WAVES;
   constexpr int WG_PER_HEAD = D / ROWS_PER_WG;
   static_assert(RPW % 2 == 0 && RPW <= 64 && D % ROWS_PER_WG == 0, "bad tiling");
-  static_assert(POOLED || !SLOTMAJOR, "slot-major order is for pooled launches");
 
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -154,47 +103,14 @@ __global__ __launch_bounds__(64 * WAVES) void gdn_decode_kernel(DecodeArgs p) {
   const int rblk = blk % WG_PER_HEAD;
   blk /= WG_PER_HEAD;
   const int h = blk % p.Hv;
-  int bi = blk / p.Hv;
+  const int bi = blk / p.Hv;
   const int row0 = rblk * ROWS_PER_WG + wave * RPW;
-
-  int64_t sunit = -1;  // slot-major: the pool slot this workgroup serves
-  if constexpr (POOLED && SLOTMAJOR) {
-    const int64_t units = p.pool_slots * p.Hv * WG_PER_HEAD;
-    if (int64_t(blockIdx.x) >= units) {
-      // Padding rows (index outside [0, pool_slots)): workgroup units + r zeroes the
-      // whole output of batch row r.
-      const int r = int(int64_t(blockIdx.x) - units);
-      const int64_t sr = p.slots[r];
-      if (sr < 0 || sr >= p.pool_slots) {
-        uint16_t* o = p.out + int64_t(r) * p.Hv * D;
-        for (int e = threadIdx.x; e < p.Hv * D; e += 64 * WAVES) o[e] = 0;
-      }
-      return;
-    }
-    int count = 0, row = -1;
-    slot_rows<WAVES>(p.slots, p.B, bi, lane, wave, count, row);
-    if (count == 0) return;  // no row names this slot
-    if (count > 1) {
-      // Rows that name one slot would update it at once: each is skipped like padding
-      // (zero output, slot untouched), decided before any state access, and counted.
-      for (int i = 0; i < p.B; ++i)
-        if (p.slots[i] == bi && lane < RPW) p.out[(int64_t(i) * p.Hv + h) * D + row0 + lane] = 0;
-      if (h == 0 && row0 == 0 && lane == 0)
-        __hip_atomic_fetch_add(&gdn_decode_pool_conflict_count, (unsigned long long)count, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-      return;
-    }
-    sunit = bi;
-    bi = row;
-  }
 
   const int64_t head = int64_t(bi) * p.Hv + h;     // index of (b, h) in v/a/b/out
   uint16_t* outp = p.out + head * D + row0;
 
   int64_t shead = head;                             // index of the state block
-  if constexpr (POOLED && SLOTMAJOR) {
-    shead = sunit * p.Hv + h;
-  } else if constexpr (POOLED) {
+  if constexpr (POOLED) {
     const int64_t slot = p.slots[bi];
     if (slot < 0 || slot >= p.pool_slots) {         // padding slot: zero output, no state
       if (lane < RPW) outp[lane] = 0;
@@ -276,11 +192,7 @@ hipError_t launch_variant(const DecodeArgs& a, hipStream_t stream) {
   const int64_t heads = int64_t(a.B) * a.Hv;
   const int64_t grid = heads * (kHeadDim / (RPW * WAVES));
   const dim3 block(64 * WAVES);
-  if (a.slots && decode_pool_slot_major(a.B, a.pool_slots, a.Hv, kHeadDim / RPW * 64)) {
-    const int64_t sgrid = a.pool_slots * a.Hv * (kHeadDim / (RPW * WAVES)) + a.B;
-    hipLaunchKernelGGL((gdn_decode_kernel<RPW, WAVES, true, true, NT, true>), dim3(unsigned(sgrid)), block, 0, stream,
-                       a);
-  } else if (a.slots) {
+  if (a.slots) {
     hipLaunchKernelGGL((gdn_decode_kernel<RPW, WAVES, true, true, NT>), dim3(grid), block, 0, stream, a);
   } else if (a.state) {
     hipLaunchKernelGGL((gdn_decode_kernel<RPW, WAVES, true, false, NT>), dim3(grid), block, 0, stream, a);
@@ -291,16 +203,6 @@ hipError_t launch_variant(const DecodeArgs& a, hipStream_t stream) {
 }
 
 }  // namespace
-
-// Pooled launches run slot-major (state blocks visited in address order) when the pool
-// has at most 4 slots per batch row, so that at most three quarters of the slot units
-// find no row, and the grid fits 32-bit work-item counts; row-major otherwise.  Config
-// 2 (512 rows over 1,024 random slots): 373.6 -> 353.5 us, the two orders timed
-// alternately in one process.
-bool decode_pool_slot_major(int64_t B, int64_t pool_slots, int Hv, int64_t items_per_head) {
-  if (B <= 0 || pool_slots <= 0 || pool_slots > 4 * B) return false;
-  return (pool_slots * Hv + B) * items_per_head <= int64_t(0xffffffffLL) && pool_slots * Hv * 128 < (int64_t(1) << 31);
-}
 
 int decode_pick_variant(int64_t heads) {
   // Measured on MI355X (B=64 and pooled B=512, cold cache): 8 rows per wave,

@@ -65,10 +65,6 @@ hipError_t launch_decode(const DecodeArgs& args, hipStream_t stream, int variant
 // is heads * decode_items_per_head(v) / block work-items).
 int decode_pick_variant(int64_t heads);
 int64_t decode_items_per_head(int variant);
-// Whether a pooled launch of B rows over pool_slots slots runs slot-major (grid units
-// per pool slot, state visited in address order, plus B workgroups for padding rows)
-// rather than row-major; items_per_head is the launch shape's work-items per head.
-bool decode_pool_slot_major(int64_t B, int64_t pool_slots, int Hv, int64_t items_per_head);
 
 // Rows of pooled decode launches on the current device that were skipped because
 // another row of their batch named the same slot, since the library was loaded or

@@ -111,11 +111,9 @@ int gdn_decode_check(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v,
  *                 marks a padding row: its output is zero and no slot is touched.
  * A slot that two or more valid rows name is a conflict: updating it from both rows
  * would race.  The kernel detects it on the device before it touches any state
- * (its workgroups scan the B indices) and skips every such row like a padding row
- * (zero output, slot untouched); gdn_decode_pool_conflicts counts the skipped rows.
- * With at most 4 pool slots per batch row the grid runs over pool slots in address
- * order (each slot's workgroups find the row that names it) rather than over rows.
- * Other arguments as gdn_decode.
+ * (each row's workgroups scan the B indices) and skips every such row like a padding
+ * row (zero output, slot untouched); gdn_decode_pool_conflicts counts the skipped
+ * rows.  Other arguments as gdn_decode.
  */
 int gdn_decode_pooled(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v,
                       float* state_pool, int64_t pool_slots,

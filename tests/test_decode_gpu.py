@@ -83,8 +83,8 @@ def test_decode_empty_batch(gpu):
 @pytest.mark.parametrize("gate", ["baseline", "slow"])
 @pytest.mark.parametrize("B", [12, 8])
 def test_decode_pooled_matches_oracle(gpu, gate, B):
-    """Pooled decode with padding rows against the oracle: B = 12 over 40 slots runs
-    slot-major (at most 4 slots per row), B = 8 row-major."""
+    """Pooled decode with padding rows against the oracle, at B = 12 and B = 8 over
+    40 slots."""
     say(f"decode pooled small gate={gate} B={B}")
     slots = 40
     w = workloads.decode_inputs(B, seed=9, gate=gate, pool_slots=slots,
@@ -110,8 +110,8 @@ def test_decode_pooled_matches_oracle(gpu, gate, B):
 
 
 def test_decode_pooled_more_rows_than_slots(gpu):
-    """24 rows over 10 slots (slot-major): rows 0-9 name every slot once, rows 10-23 are
-    padding (negative or past the pool), written by the grid's padding workgroups."""
+    """24 rows over 10 slots: rows 0-9 name every slot once, rows 10-23 are padding
+    (negative or past the pool) with zero output."""
     say("decode pooled: 24 rows over 10 slots")
     slots, B = 10, 24
     w = workloads.decode_inputs(B, seed=77, gate="slow", pool_slots=24, state_scale=1.0)
@@ -173,7 +173,7 @@ def test_decode_pooled_duplicate_slots(gpu, heads, B, slots):
     conflicting row has zero output and its slot keeps its bits; every other row matches
     the oracle; gdn_decode_pool_conflicts counts the five skipped rows.  The layouts take
     one-wave (B*Hv < 128) and four-wave workgroups, over several scan passes for B = 1500,
-    slot-major (at most 4 slots per row) and row-major (8 over 40, 1500 over 8000)."""
+    and pools of 3 to 5 slots per row."""
     say(f"decode pooled duplicate slots heads={heads} B={B} slots={slots}")
     w = workloads.decode_inputs(B, Heads(*heads), seed=40 + B, gate="slow", pool_slots=slots,
                                 state_scale=1.0)
@@ -286,7 +286,7 @@ def test_decode_every_launch_shape(gpu):
 def test_decode_pooled_duplicates_every_launch_shape(gpu, slots):
     """Every compiled launch shape on a pooled batch of 5 rows whose rows 0 and 3 share a
     slot: both rows skipped (zero output, slot bit-identical), the others against the
-    oracle, and two conflicts counted per launch; 11 slots run slot-major, 30 row-major."""
+    oracle, and two conflicts counted per launch, over pools of 11 and 30 slots."""
     lib = _lib.load()
     stream = torch.cuda.current_stream(gpu).cuda_stream
     ptr = lambda t: None if t is None else t.data_ptr()
