@@ -149,14 +149,25 @@ struct PrepVariant {
   static constexpr int VSEG = 0;
 };
 
-// Prepared tiles of one chunk-head in the workspace: the LDS images of T~ hi,
-// T~ lo and P, in that order (strictly-upper blocks zero), then the chunk's gates
-// beta_c, e^{gamma_c} and e^{gamma_last - gamma_c} (fp32, 64 each), in 16-byte
-// units.  Chunk t of sequence s, v-head h is image (s TC + t) Hv + h, TC = ceil(T /
-// C) (a sequence clamped into [0, T] has at most TC chunks).
-constexpr int kTileUnits = 3 * C * TSTR / 8;
+// Prepared tiles of one chunk-head in the workspace, in 16-byte units: of the LDS
+// tiles of T~ hi, T~ lo and P, in that order, the part that the state pass reads
+// (the operand rows of the lower-triangular block pairs): rows 0 .. 31, columns
+// 0 .. 31 (4 units a row), then rows 32 .. 63, columns 0 .. 63 (8 units a row), in
+// the tiles' permuted column order, strictly-upper blocks zero; then the chunk's
+// gates beta_c, e^{gamma_c} and e^{gamma_last - gamma_c} (fp32, 64 each).  The
+// rest of each tile (columns 32 .. 63 of rows 0 .. 31, and the row padding) stays
+// zero in the state pass's LDS.  Chunk t of sequence s, v-head h is image (s TC +
+// t) Hv + h, TC = ceil(T / C) (a sequence clamped into [0, T] has at most TC chunks).
+constexpr int kTileUnits1 = 32 * 4 + 32 * 8;  // units of one tile
+constexpr int kTileUnits = 3 * kTileUnits1;
 constexpr int kGateUnits = 3 * C / 4;
 constexpr int kTileImage = kTileUnits + kGateUnits;
+
+// Element offset, from the tile's base, of unit e (0 .. kTileUnits1 - 1) of a tile's
+// part of an image.
+__device__ __forceinline__ int tile_unit_off(int e) {
+  return e < 128 ? (e >> 2) * TSTR + 8 * (e & 3) : (32 + ((e - 128) >> 3)) * TSTR + 8 * ((e - 128) & 7);
+}
 constexpr int kMaxSortedSeqs = 1024;  // longest-first ordering up to this many sequences
 constexpr int kMaxPersistList = 128;  // chains per workgroup of the persistent kernel
 constexpr int kMaxPersistLpt = 64;    // batches of at most this many sequences get a longest-processing-time list
@@ -954,16 +965,18 @@ __device__ __forceinline__ float* gate_unit(const ChunkBufs& cb, int g) {
   return cb.bet + (g >> 4) * (Smem::kParities * C) + 4 * (g & 15);
 }
 
-// Producer thread pt's share of a chunk's T~ hi, T~ lo and P tiles (their LDS
-// images) and gates to the chunk's image in the workspace; NaN images once a
-// hand-off wait of the workgroup gave up.  The gates go out from the first wave,
-// which stores the next chunk's gates after this copy.
+// Producer thread pt's share of a chunk's T~ hi, T~ lo and P tiles (the parts of
+// their LDS tiles that the state pass reads) and gates to the chunk's image in the
+// workspace; NaN images once a hand-off wait of the workgroup gave up.  The gates go
+// out from the first wave, which stores the next chunk's gates after this copy.
 template <class Smem>
 __device__ __forceinline__ void copy_tiles_out(const ChunkBufs& cb, u32x4* image, int pt, bool poison) {
-  constexpr int NT1 = C * TSTR / 8;
+  constexpr int NT1 = kTileUnits1;
   constexpr u32x4 nan4 = u32x4{kNaNx2, kNaNx2, kNaNx2, kNaNx2};
   for (int e = pt; e < kTileUnits; e += NPROD) {
-    const uint16_t* src = e < NT1 ? cb.Th + 8 * e : e < 2 * NT1 ? cb.Tl + 8 * (e - NT1) : cb.P + 8 * (e - 2 * NT1);
+    const uint16_t* src = e < NT1       ? cb.Th + tile_unit_off(e)
+                          : e < 2 * NT1 ? cb.Tl + tile_unit_off(e - NT1)
+                                        : cb.P + tile_unit_off(e - 2 * NT1);
     image[e] = poison ? nan4 : *reinterpret_cast<const u32x4*>(src);
   }
   if (pt < kGateUnits)
@@ -1414,7 +1427,7 @@ __device__ __forceinline__ void loader_loop(PrefillSmem& sm, const PrefillArgs& 
                                             int lane0) {
   constexpr int NVIT = (V::VSEG + NPROD - 1) / NPROD;        // V segments per loader thread
   constexpr int NTIT = (kTileImage + NPROD - 1) / NPROD;     // 16-byte tile units per loader thread
-  constexpr int NT1 = C * TSTR / 8;                          // 16-byte units per tile
+  constexpr int NT1 = kTileUnits1;                           // 16-byte units per tile image
   const int pt = pw * 64 + lane0;
   const LaneOffsets lo = {(pt >> 4) * p.Hk * D + 8 * (pt & 15), (pt >> 4) * p.Hq * D + 8 * (pt & 15), pt * p.Hv};
   int voff[NVIT], vrow[NVIT];
@@ -1468,7 +1481,9 @@ __device__ __forceinline__ void loader_loop(PrefillSmem& sm, const PrefillArgs& 
     for (int it = 0; it < NTIT; ++it) {
       const int e = pt + it * NPROD;
       if (e < kTileUnits) {
-        uint16_t* dst = e < NT1 ? cb.Th + 8 * e : e < 2 * NT1 ? cb.Tl + 8 * (e - NT1) : cb.P + 8 * (e - 2 * NT1);
+        uint16_t* dst = e < NT1       ? cb.Th + tile_unit_off(e)
+                        : e < 2 * NT1 ? cb.Tl + tile_unit_off(e - NT1)
+                                      : cb.P + tile_unit_off(e - 2 * NT1);
         *reinterpret_cast<u32x4*>(dst) = tv[it];
       } else if (e < kTileImage) {
         *reinterpret_cast<u32x4*>(gate_unit<PrefillSmem>(cb, e - kTileUnits)) = tv[it];
@@ -1947,10 +1962,11 @@ __device__ int pick_sequence(PrefillSmem& sm, const PrefillArgs& p, int rank, in
 }
 
 // Workgroup b handles slice f of chain `chain` (chain = rank-major, v-head
-// minor).  With F > 1 the F slices of a chain are b = 8 F (chain / 8) + 8 f +
-// chain % 8: workgroups are dealt to the XCDs round-robin, so the slices of one
-// chain share an XCD (and its L2) for their common K/Q/V reads.  With F == 1 the
-// two chains of a GQA pair share an XCD the same way.
+// minor).  With F > 1 the F slices of chain c are b = 16 F (c / 16) + 8 (F (c % 2)
+// + f) + (c % 16) / 2: workgroups are dealt to the XCDs round-robin, so the slices
+// of one chain, and those of its GQA partner (chain c ^ 1), share an XCD (and its
+// L2) for their common K/Q reads.  With F == 1 the two chains of a GQA pair share an
+// XCD the same way.
 template <class V>
 __global__ __launch_bounds__(V::NTHREADS) void gdn_prefill_kernel(PrefillArgs p) {
   constexpr int NCW = V::NCW, VT = V::VT, VW = V::VW, NTHREADS = V::NTHREADS;
@@ -1977,13 +1993,15 @@ __global__ __launch_bounds__(V::NTHREADS) void gdn_prefill_kernel(PrefillArgs p)
                    : hw == 3 ? 0 : hw < 3 ? hw + 1 : hw;
 
   const int bid = blockIdx.x;
-  // F == 1: blocks b and b + 8 of each group of 16 take chains 2m and 2m + 1 (v-heads
-  // 2j, 2j + 1, which read the same K and Q): workgroups are dealt to the 8 XCDs
-  // round-robin, so the two start together on one XCD and share its L2.
+  // Workgroups are dealt to the 8 XCDs round-robin.  F == 1: blocks b and b + 8 of
+  // each group of 16 take chains 2m and 2m + 1 (v-heads 2j, 2j + 1, which read the
+  // same K and Q), so the two start together on one XCD and share its L2.  F > 1:
+  // in each group of 16 F blocks, the 2 F blocks b = 8 l + x (l = 0 .. 2F - 1) of
+  // XCD x take slice l % F of chain 2x + l / F: both chains of a pair, all slices.
   const int chain = V::F == 1 ? (bid & ~15) | ((bid & 7) << 1) | ((bid >> 3) & 1)
-                              : (bid / (8 * V::F)) * 8 + bid % 8;
+                              : (bid / (16 * V::F)) * 16 + 2 * (bid % 8) + (bid / 8) % (2 * V::F) / V::F;
   const int row0 = V::F == 1 ? 0 : ((bid / 8) % V::F) * V::ROWS;
-  if (chain >= p.N * p.Hv) return;  // padding of the last group of eight chains (workgroup-uniform)
+  if (chain >= p.N * p.Hv) return;  // padding of the last group of 16 chains (workgroup-uniform)
   const int h = chain % p.Hv;
   const int seq = pick_sequence<NTHREADS>(sm, p, chain / p.Hv, tid);
   const int hq = h / (p.Hv / p.Hq);
@@ -2347,8 +2365,8 @@ __global__ __launch_bounds__(V::NTHREADS) void gdn_prefill_persistent_kernel(Pre
   }
 }
 
-// Prep kernel of the two-kernel path (few chains).  Workgroup b = (s R' + r) Hv + h
-// prepares chunks r p.prep_chunks .. (r + 1) p.prep_chunks - 1 of sequence s for
+// Prep kernel of the two-kernel path (few chains).  Item (s R' + r) Hv + h (the
+// workgroup index paired as below) prepares chunks r p.prep_chunks .. (r + 1) p.prep_chunks - 1 of sequence s for
 // v-head h (R' = ceil(TC / p.prep_chunks)): the producer waves run their loop over
 // those chunks and copy each one's T~ hi, T~ lo and P tiles (LDS images) to its
 // image in p.tiles; their loads of chunk t + 1 are in flight meanwhile.  Its LDS
@@ -2364,7 +2382,12 @@ __global__ __launch_bounds__(PrepVariant::NTHREADS) void gdn_prefill_prep_kernel
   const int64_t tc = (p.T + C - 1) / C;
   const int run = p.prep_chunks;
   const int64_t runs = (tc + run - 1) / run;
-  const int64_t bid = blockIdx.x;
+  // Workgroups are dealt to the 8 XCDs round-robin: blocks b and b + 8 of each group
+  // of 16 take items 2m and 2m + 1 (v-heads 2j and 2j + 1 of one run, which read the
+  // same K and Q), so the two share an XCD's L2.
+  const int64_t b = blockIdx.x;
+  const int64_t bid = (b & ~int64_t(15)) | ((b & 7) << 1) | ((b >> 3) & 1);
+  if (bid >= int64_t(p.N) * runs * p.Hv) return;  // padding of the last group of 16 (workgroup-uniform)
   const int h = int(bid % p.Hv);
   const int seq = int(bid / p.Hv / runs), r = int(bid / p.Hv % runs);
   int64_t s0 = load_cu(p.cu_seqlens, p.cu_is_64, seq);
@@ -2401,7 +2424,7 @@ __global__ __launch_bounds__(PrepVariant::NTHREADS) void gdn_prefill_prep_kernel
 template <class V>
 hipError_t launch_variant(const PrefillArgs& a, hipStream_t stream, hipEvent_t done = nullptr) {
   const int64_t chains = int64_t(a.N) * a.Hv;
-  const int64_t grid = V::F == 1 ? (chains + 15) / 16 * 16 : (chains + 7) / 8 * 8 * V::F;
+  const int64_t grid = (chains + 15) / 16 * 16 * V::F;
   if (done != nullptr) {
     hipExtLaunchKernelGGL(gdn_prefill_kernel<V>, dim3(unsigned(grid)), dim3(V::NTHREADS), 0, stream, nullptr, done, 0,
                           a);
@@ -2615,7 +2638,7 @@ int split_factor(int64_t chains) {
 int64_t prefill_work_items(int64_t chains) {
   if (chains <= 0) return 0;
   const int F = split_factor(chains);
-  const int64_t grid = F == 1 ? (chains + 15) / 16 * 16 : (chains + 7) / 8 * 8 * F;
+  const int64_t grid = (chains + 15) / 16 * 16 * F;
   switch (F) {
     case 1: return grid * SplitVariant1<false>::NTHREADS;
     case 2: return grid * SplitVariant2<false>::NTHREADS;
@@ -2628,7 +2651,7 @@ namespace {
 // Largest workspace the two-kernel path uses; bigger batches take one kernel.
 constexpr int64_t kMaxWorkspaceBytes = int64_t(2) << 30;
 // Images above this size are read back mostly from HBM by the state pass.
-constexpr int64_t kDeepImageBytes = int64_t(96) << 20;
+constexpr int64_t kDeepImageBytes = int64_t(64) << 20;
 }  // namespace
 
 // Batches split 4 or 8 ways repeat the producer work in every slice of a chain and
@@ -2667,15 +2690,17 @@ hipError_t launch_prefill(const PrefillArgs& a, hipStream_t stream, hipEvent_t d
     const int64_t run = (chunks * a.Hv + slots - 1) / slots;
     PrefillArgs b = a;
     b.prep_chunks = int(run < 1 ? 1 : run > tc ? tc : run);
-    const int64_t grid = int64_t(a.N) * ((tc + b.prep_chunks - 1) / b.prep_chunks) * a.Hv;
+    const int64_t grid = (int64_t(a.N) * ((tc + b.prep_chunks - 1) / b.prep_chunks) * a.Hv + 15) / 16 * 16;
     hipLaunchKernelGGL(gdn_prefill_prep_kernel, dim3(unsigned(grid)), dim3(PrepVariant::NTHREADS), 0, stream, b);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
     if (F == 4) return launch_variant<Variant<2, 1, false, true>>(a, stream, done);
     // Split 8 ways, images beyond what the caches keep between the two kernels are
-    // loaded two chunks ahead (one sequence of 8,192 tokens, 116 MB of images: 283 ->
-    // 272 us; 16,384 tokens 609 -> 581 us; 6,000 tokens, 85 MB: 188 -> 190 us).  Split
-    // 4 ways it measured no change (two 4,096-token sequences: 186.2 -> 185.8 us).
+    // loaded two chunks ahead (one sequence, 32 v-heads, 19,200-byte images: 12,288
+    // tokens, 118 MB of images, 420.1 -> 396.9 us; 10,500 tokens 349.8 -> 333.8;
+    // 8,192 tokens, 79 MB, 255.7 -> 252.5; 6,000 tokens, 58 MB, 187.8 -> 188.0).
+    // Split 4 ways it measured no change (two 4,096-token sequences, images of whole
+    // tiles: 186.2 -> 185.8 us).
     if (prefill_workspace_bytes(a.N, a.T, a.Hv) > kDeepImageBytes)
       return launch_variant<Variant<4, 1, false, true, 4, false, true, true>>(a, stream, done);
     return launch_variant<Variant<4, 1, false, true, 4, false, true>>(a, stream, done);

@@ -164,9 +164,9 @@ int64_t gdn_static_device_bytes(void);
  * tokens, whose chains the launcher splits over several workgroups, runs the
  * two-kernel path of gdn_prefill_with_workspace (each chunk prepared once) in a
  * scratch array the library holds on each device (GDN_PREFILL_DROPIN_SCRATCH_BYTES,
- * its own, not gdn_prefill_no_alloc's), when its chunk images fit: 28,416 bytes per
- * 64-token chunk and v-head, so with 32 v-heads sequences of up to 9,408 tokens
- * (BASELINE's 4,096-token sequence needs 55.5 MiB).  Longer sequences run one
+ * its own, not gdn_prefill_no_alloc's), when its chunk images fit: 19,200 bytes per
+ * 64-token chunk and v-head, so with 32 v-heads sequences of up to 13,952 tokens
+ * (BASELINE's 4,096-token sequence needs 37.5 MiB).  Longer sequences run one
  * kernel (16,384 tokens: about 8 % slower than two).  The results are the same bit
  * for bit either way.  The library orders those launches on the device (each
  * waits, on its stream, for an event that the previous one records as it

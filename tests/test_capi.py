@@ -178,12 +178,13 @@ def test_prefill_fault_injection_rejects(lib, kw, code, frag):
 
 
 def test_prefill_workspace_size(lib):
-    """Bytes of the two-kernel prefill path: N ceil(T / 64) Hv chunk images of 28,416
-    bytes (T~ hi, T~ lo and P, 64 x 72 bf16 each, then three 64-float gate vectors) for
-    batches whose chains are split 4 or 8 ways across workgroups (at most 64 chains on
-    256 CUs), 0 otherwise.  Without a GPU the CU count defaults to 256."""
-    image = 3 * 64 * 72 * 2 + 3 * 64 * 4
-    assert image == 28416
+    """Bytes of the two-kernel prefill path: N ceil(T / 64) Hv chunk images of 19,200
+    bytes (of T~ hi, T~ lo and P each the operand rows the state pass reads: 32 rows of
+    32 and 32 rows of 64 bf16; then three 64-float gate vectors) for batches whose chains
+    are split 4 or 8 ways across workgroups (at most 64 chains on 256 CUs), 0 otherwise.
+    Without a GPU the CU count defaults to 256."""
+    image = 3 * (32 * 32 + 32 * 64) * 2 + 3 * 64 * 4
+    assert image == 19200
     assert lib.gdn_prefill_workspace_size(1, 4096, 32) == 64 * 32 * image
     assert lib.gdn_prefill_workspace_size(3, 100, 8) == 3 * 2 * 8 * image
     assert lib.gdn_prefill_workspace_size(2, 4096, 32) == 2 * 64 * 32 * image    # 64 chains
@@ -301,7 +302,7 @@ def test_static_device_bytes_match_the_header(lib):
     assert _lib.GDN_PREFILL_NO_ALLOC_SCRATCH_BYTES == 64 << 20
     assert want == (192 << 20) + 12
     # the drop-in array holds config 3's images (one 4,096-token sequence, 32 v-heads)
-    # and those of one sequence of up to 9,408 tokens
+    # and those of one sequence of up to 13,952 tokens
     assert lib.gdn_prefill_workspace_size(1, 4096, 32) <= _lib.GDN_PREFILL_DROPIN_SCRATCH_BYTES
-    assert lib.gdn_prefill_workspace_size(1, 9408, 32) <= _lib.GDN_PREFILL_DROPIN_SCRATCH_BYTES
-    assert lib.gdn_prefill_workspace_size(1, 9409, 32) > _lib.GDN_PREFILL_DROPIN_SCRATCH_BYTES
+    assert lib.gdn_prefill_workspace_size(1, 13952, 32) <= _lib.GDN_PREFILL_DROPIN_SCRATCH_BYTES
+    assert lib.gdn_prefill_workspace_size(1, 13953, 32) > _lib.GDN_PREFILL_DROPIN_SCRATCH_BYTES

@@ -611,13 +611,13 @@ def test_prefill_dropin_scratch_path(gpu, in_place):
 
 
 def test_prefill_dropin_long_sequence(gpu):
-    """An 8,192-token sequence (32 v-heads: 116 MB of chunk images, more than 64 MiB, and
-    loaded two chunks ahead by the state pass) runs two kernels in the drop-in's scratch:
-    against the oracle, and bit for bit equal to gdn_prefill_with_workspace."""
-    say("prefill drop-in, one 8,192-token sequence")
+    """A 12,288-token sequence (32 v-heads: 118 MB of chunk images, more than 64 MiB, so
+    the state pass loads them two chunks ahead) runs two kernels in the drop-in's
+    scratch: against the oracle, and bit for bit equal to gdn_prefill_with_workspace."""
+    say("prefill drop-in, one 12,288-token sequence")
     lib = _lib.load()
-    p = workloads.prefill_inputs([8192], seed=62, gate="slow", state_scale=0.5)
-    need = lib.gdn_prefill_workspace_size(1, 8192, 32)
+    p = workloads.prefill_inputs([12288], seed=62, gate="slow", state_scale=0.5)
+    need = lib.gdn_prefill_workspace_size(1, 12288, 32)
     assert 64 << 20 < need <= _lib.GDN_PREFILL_DROPIN_SCRATCH_BYTES, need
     o_ref, s_ref = oracle_prefill(p)
     out, ns = run_prefill(p, gpu)

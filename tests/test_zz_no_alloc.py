@@ -57,7 +57,7 @@ def test_prefill_no_alloc_matches_workspace_entry_point(gpu):
 
 def test_prefill_no_alloc_rejects_batches_beyond_its_scratch(gpu):
     lib = _lib.load()
-    p = workloads.prefill_inputs([4096, 4096], seed=53)     # 64 chains: 116 MB of chunk images
+    p = workloads.prefill_inputs([4096, 4096], seed=53)     # 64 chains: 78.6 MB of chunk images
     need = lib.gdn_prefill_workspace_size(2, 8192, 32)
     assert need > SCRATCH_BYTES
     say("prefill no-alloc: batch beyond the scratch is rejected")
