@@ -1476,7 +1476,6 @@ __device__ __forceinline__ void loader_loop(PrefillSmem& sm, const PrefillArgs& 
     const ChunkBufs cb = chunk_bufs(sm, t & 1);
     if (t >= 2) wait_count<V::kHooks>(sm, kConsumed, V::NCW * (t - 1));  // chunk t - 2 consumed
     stage_kq(cb, f, pt);
-    if (ncs < s1) producer_prefetch(p, ncs, nclen, h, hq, hk, pt, lo, f);
 #pragma unroll
     for (int it = 0; it < NTIT; ++it) {
       const int e = pt + it * NPROD;
@@ -1489,11 +1488,6 @@ __device__ __forceinline__ void loader_loop(PrefillSmem& sm, const PrefillArgs& 
         *reinterpret_cast<u32x4*>(gate_unit<PrefillSmem>(cb, e - kTileUnits)) = tv[it];
       }
     }
-    if (deep && t + 2 < nchunks) {  // chunk t + 2's images into this set
-      const u32x4* src = tiles + int64_t(t + 2) * p.Hv * kTileImage;
-#pragma unroll
-      for (int it = 0; it < NTIT; ++it) tv[it] = src[toff[it]];
-    }
     if (t >= 1) wait_count<V::kHooks>(sm, kVFree, V::NCW * t);  // the consumers' last read of V
 #pragma unroll
     for (int it = 0; it < NVIT; ++it) {
@@ -1502,6 +1496,16 @@ __device__ __forceinline__ void loader_loop(PrefillSmem& sm, const PrefillArgs& 
         *reinterpret_cast<u32x4*>(sm.V + (seg / (V::ROWS / 8)) * VSTR + 8 * (seg % (V::ROWS / 8))) = fv[it];
     }
     signal_count(sm, kReady, lane);
+    // The next chunks' loads go out after the hand-off.  Issued before it, the
+    // waits for this tick's registers (loaded a tick earlier) would also wait for
+    // them: the K/Q loads are conditional, so the compiler cannot count them and
+    // waits for every load issued since.
+    if (ncs < s1) producer_prefetch(p, ncs, nclen, h, hq, hk, pt, lo, f);
+    if (deep && t + 2 < nchunks) {  // chunk t + 2's images into this set
+      const u32x4* src = tiles + int64_t(t + 2) * p.Hv * kTileImage;
+#pragma unroll
+      for (int it = 0; it < NTIT; ++it) tv[it] = src[toff[it]];
+    }
     if (t + 1 < nchunks) {  // chunk t + 1's V slice (and images) into registers
       if (!deep) {
         const u32x4* src = tiles + int64_t(t + 1) * p.Hv * kTileImage;
