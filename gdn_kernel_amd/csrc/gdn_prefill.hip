@@ -972,15 +972,24 @@ __device__ __forceinline__ float* gate_unit(const ChunkBufs& cb, int g) {
 template <class Smem>
 __device__ __forceinline__ void copy_tiles_out(const ChunkBufs& cb, u32x4* image, int pt, bool poison) {
   constexpr int NT1 = kTileUnits1;
+  constexpr int NIT = (kTileUnits + NPROD - 1) / NPROD;
   constexpr u32x4 nan4 = u32x4{kNaNx2, kNaNx2, kNaNx2, kNaNx2};
-  for (int e = pt; e < kTileUnits; e += NPROD) {
+  // All LDS reads first (one round of latency), then the stores; units past the
+  // tiles (last round) re-read the last unit and store nothing.
+  u32x4 v[NIT];
+#pragma unroll
+  for (int it = 0; it < NIT; ++it) {
+    const int e = pt + it * NPROD < kTileUnits ? pt + it * NPROD : kTileUnits - 1;
     const uint16_t* src = e < NT1       ? cb.Th + tile_unit_off(e)
                           : e < 2 * NT1 ? cb.Tl + tile_unit_off(e - NT1)
                                         : cb.P + tile_unit_off(e - 2 * NT1);
-    image[e] = poison ? nan4 : *reinterpret_cast<const u32x4*>(src);
+    v[it] = *reinterpret_cast<const u32x4*>(src);
   }
-  if (pt < kGateUnits)
-    image[kTileUnits + pt] = poison ? nan4 : *reinterpret_cast<const u32x4*>(gate_unit<Smem>(cb, pt));
+  const u32x4 gv = pt < kGateUnits ? *reinterpret_cast<const u32x4*>(gate_unit<Smem>(cb, pt)) : nan4;
+#pragma unroll
+  for (int it = 0; it < NIT; ++it)
+    if (pt + it * NPROD < kTileUnits) image[pt + it * NPROD] = poison ? nan4 : v[it];
+  if (pt < kGateUnits) image[kTileUnits + pt] = poison ? nan4 : gv;
 }
 
 // Persistent kernel: the number of chains in the workgroup's list, and the first
@@ -1005,8 +1014,10 @@ __device__ __forceinline__ int next_chain(Smem& sm, int k) {
 // state rows [row0, row0 + ROWS) only.
 // With V::kCopy (the prep kernel, no consumers) the producers also write each
 // chunk's tiles to images (chunk t of the run at images + t Hv kTileImage): chunk
-// t - 1's at the start of tick t, once all four waves have handed it over, and
-// before the staging barrier, after which tick t writes the same buffers.
+// t - 1's in step 1 of tick t, once all four waves have handed it over (so also
+// done with its K and Q, which the staging overwrites), and before the staging
+// barrier, after which tick t writes the same tiles; the first wave copies the
+// gates out before it stores the next chunk's.
 template <class V, class Smem>
 __device__ __forceinline__ void producer_loop(Smem& sm, const PrefillArgs& p, int64_t s0, int64_t s1,
                                               int nchunks, int h, int hq, int hk, int row0, int pw, int lane0,
@@ -1078,14 +1089,17 @@ __device__ __forceinline__ void producer_loop(Smem& sm, const PrefillArgs& p, in
     constexpr int kPar = Smem::kParities;
     if (u >= kPar) wait_count<V::kHooks>(sm, kConsumed, V::NCW * (u - kPar + 1));
     if constexpr (V::kCopy) {
-      if (t >= 1) {
-        wait_count<V::kHooks>(sm, kReady, 4 * t);  // chunk t - 1 handed over by all four waves
-        copy_tiles_out<Smem>(chunk_bufs(sm, (t - 1) & 1), images + int64_t(t - 1) * p.Hv * kTileImage, pt, aborted(sm));
-      }
+      if (t >= 1) wait_count<V::kHooks>(sm, kReady, 4 * t);  // chunk t - 1 handed over by all four waves
     }
 
     // 1: stage K/Q (permuted columns), gates
     stage_kq(cb, f, pt);
+    if constexpr (V::kCopy) {
+      // Chunk t - 1's tiles out, after the staging: its stores are counted with the
+      // loads, and the staging's wait for its registers would wait for them too.
+      if (t >= 1)
+        copy_tiles_out<Smem>(chunk_bufs(sm, (t - 1) & 1), images + int64_t(t - 1) * p.Hv * kTileImage, pt, aborted(sm));
+    }
     if (pw == 0) store_gates(cb, gts, lane);
     // The V slice of this chunk into registers; staged at the end of the tick,
     // after the consumers' last read of the previous chunk's V.
