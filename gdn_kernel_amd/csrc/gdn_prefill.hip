@@ -486,7 +486,7 @@ __device__ unsigned int gdn_prefill_giveup_count;
 namespace {
 
 // Hand-off between the two roles: monotonically increasing LDS counters.  A wave
-// signals by adding 1 after all its earlier LDS accesses completed (release); a
+// signals by adding 1 after its earlier LDS accesses (release: see signal_count); a
 // waiter polls until the count reaches its target (acquire).
 enum SyncCounter {
   kReady = 0,     // chunk handed over to the consumers (4 a chunk; pipelined: its T~ and P, NS + 2)
@@ -505,10 +505,20 @@ enum SyncCounter {
 };
 constexpr int kSpinLimit = 1 << 21;  // default polls (about 70 ms) before a wait gives up
 
+// Every hand-off publishes LDS data (or releases LDS reads) to waves of the same
+// workgroup, through an LDS counter.  The LDS performs a CU's operations in one
+// order, and a wave's own LDS operations in the order the wave issues them, so the
+// increment is performed after every LDS write or read the wave issued before it,
+// and a waiter that sees the count issues its reads after that.  No wait for the
+// wave's outstanding LDS operations is needed before the increment (a workgroup-
+// scope release fence would add one, s_waitcnt lgkmcnt(0), which stalls the
+// signalling wave until its last writes land); the compiler-level fences keep the
+// program order.  Nothing is published through these counters in global memory.
 template <class Smem>
 __device__ __forceinline__ void signal_count(Smem& sm, int which, int lane) {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "workgroup");
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
   if (lane == 0) __hip_atomic_fetch_add(&sm.sync[which], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
+  __atomic_signal_fence(__ATOMIC_SEQ_CST);
 }
 
 // Waits until counter `which` reaches `target`.  Every wait is bounded: if one
