@@ -1441,10 +1441,12 @@ __device__ __forceinline__ void producer_loop_split(PrefillSmem& sm, const Prefi
 // = image of chunk 0 of this chain; chunk t is Hv images further) instead of
 // computed.  K and Q are staged as the producers stage them, V at the end of the
 // tick, after the consumers' last read of the previous chunk's V.
-// The images and V of chunk t + 1 are loaded into registers during tick t, so
-// their latency overlaps the waits for the consumers; with V::kDeepImages the
-// images of chunk t + 2 (two register sets, alternating), as soon as chunk t's are
-// in LDS.
+// The images of chunk t + 1 are loaded into registers during tick t, so their
+// latency overlaps the waits for the consumers; with V::kDeepImages the images of
+// chunk t + 2 (two register sets, alternating), as soon as chunk t's are in LDS.
+// V goes two chunks ahead in every variant (two register sets): the prep kernel does
+// not read V, so with inputs that the caches do not hold its loads come from HBM
+// (config 3 with four rotating input sets: 142.5 -> 132.0 us, unchanged with one).
 template <class V>
 __device__ __forceinline__ void loader_loop(PrefillSmem& sm, const PrefillArgs& p, const u32x4* tiles, int64_t s0,
                                             int64_t s1, int nchunks, int h, int hq, int hk, int row0, int pw,
@@ -1468,10 +1470,21 @@ __device__ __forceinline__ void loader_loop(PrefillSmem& sm, const PrefillArgs& 
   for (int it = 0; it < NTIT; ++it) toff[it] = pt + it * NPROD < kTileImage ? pt + it * NPROD : kTileImage - 1;
   // (First-class vectors: copies of uint4 structs would go through the stack.)
   constexpr bool deep = V::kDeepImages;
-  u32x4 tva[NTIT], tvb[deep ? NTIT : 1], fv[NVIT];
+  u32x4 tva[NTIT], tvb[deep ? NTIT : 1], fva[NVIT], fvb[NVIT];
+  // V slice of chunk t (tokens [s0 + C t, s1) of it) into fv, zero past the sequence.
+  auto load_v = [&](int t, u32x4(&fv)[NVIT]) {
+    const int64_t vs = s0 + int64_t(t) * C;
+    const int vlen = int(s1 - vs < C ? s1 - vs : C);
+    const uint16_t* vb = p.v + (vs * p.Hv + h) * D + row0;
+#pragma unroll
+    for (int it = 0; it < NVIT; ++it) {
+      fv[it] = u32x4{0u, 0u, 0u, 0u};
+      if (vrow[it] < vlen) fv[it] = *reinterpret_cast<const u32x4*>(vb + voff[it]);
+    }
+  };
   ProducerPrefetch f;
   producer_prefetch(p, s0, int(s1 - s0 < C ? s1 - s0 : C), h, hq, hk, pt, lo, f);
-  // Chunk 0's images (and chunk 1's) and chunk 0's V slice into registers.
+  // Chunk 0's images (and chunk 1's), and the V slices of chunks 0 and 1, into registers.
 #pragma unroll
   for (int it = 0; it < NTIT; ++it) tva[it] = tiles[toff[it]];
   if constexpr (deep) {
@@ -1481,17 +1494,13 @@ __device__ __forceinline__ void loader_loop(PrefillSmem& sm, const PrefillArgs& 
       for (int it = 0; it < NTIT; ++it) tvb[it] = src[toff[it]];
     }
   }
-  {
-    const int clen0 = int(s1 - s0 < C ? s1 - s0 : C);
-    const uint16_t* vb = p.v + (s0 * p.Hv + h) * D + row0;
-#pragma unroll
-    for (int it = 0; it < NVIT; ++it) {
-      fv[it] = u32x4{0u, 0u, 0u, 0u};
-      if (vrow[it] < clen0) fv[it] = *reinterpret_cast<const u32x4*>(vb + voff[it]);
-    }
-  }
+  load_v(0, fva);
+  if (nchunks > 1) load_v(1, fvb);
 
-  auto tick = [&](int t, u32x4(&tv)[NTIT]) {
+  // Tick t stages chunk t from the register sets tv (images) and fv (V), then loads
+  // chunk t + 2's V into fv (the V loads go two chunks ahead, so that their latency
+  // from HBM, when the inputs are not in the caches, stays off the chain).
+  auto tick = [&](int t, u32x4(&tv)[NTIT], u32x4(&fv)[NVIT]) {
     int lane = lane0;
     asm volatile("" : "+v"(lane));
     const int64_t cs = s0 + int64_t(t) * C;
@@ -1530,27 +1539,22 @@ __device__ __forceinline__ void loader_loop(PrefillSmem& sm, const PrefillArgs& 
 #pragma unroll
       for (int it = 0; it < NTIT; ++it) tv[it] = src[toff[it]];
     }
-    if (t + 1 < nchunks) {  // chunk t + 1's V slice (and images) into registers
-      if (!deep) {
-        const u32x4* src = tiles + int64_t(t + 1) * p.Hv * kTileImage;
+    if (!deep && t + 1 < nchunks) {  // chunk t + 1's images into registers
+      const u32x4* src = tiles + int64_t(t + 1) * p.Hv * kTileImage;
 #pragma unroll
-        for (int it = 0; it < NTIT; ++it) tv[it] = src[toff[it]];
-      }
-      const uint16_t* vb = p.v + (ncs * p.Hv + h) * D + row0;
-#pragma unroll
-      for (int it = 0; it < NVIT; ++it) {
-        fv[it] = u32x4{0u, 0u, 0u, 0u};
-        if (vrow[it] < nclen) fv[it] = *reinterpret_cast<const u32x4*>(vb + voff[it]);
-      }
+      for (int it = 0; it < NTIT; ++it) tv[it] = src[toff[it]];
     }
+    if (t + 2 < nchunks) load_v(t + 2, fv);  // chunk t + 2's V slice
   };
-  if constexpr (deep) {
-    for (int t = 0; t < nchunks; t += 2) {
-      tick(t, tva);
-      if (t + 1 < nchunks) tick(t + 1, tvb);
+  for (int t = 0; t < nchunks; t += 2) {
+    tick(t, tva, fva);
+    if (t + 1 < nchunks) {
+      if constexpr (deep) {
+        tick(t + 1, tvb, fvb);
+      } else {
+        tick(t + 1, tva, fvb);
+      }
     }
-  } else {
-    for (int t = 0; t < nchunks; ++t) tick(t, tva);
   }
 }
 
