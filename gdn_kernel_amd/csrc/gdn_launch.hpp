@@ -84,9 +84,10 @@ hipError_t launch_prefill(const PrefillArgs& args, hipStream_t stream, hipEvent_
 constexpr int64_t kPrefillScratchBytes = int64_t(64) << 20;
 hipError_t prefill_scratch(void** ptr);
 
-// The drop-in gdn_prefill's launcher: launch_prefill, except that one sequence of at
-// least kDropinTwoKernelTokens tokens runs the two-kernel path in a per-device scratch
-// of the library (kPrefillDropinScratchBytes), ordered between launches by an event.
+// The drop-in gdn_prefill's launcher: launch_prefill, except that a batch of few
+// chains whose sequences average at least kDropinTwoKernelTokens tokens runs the
+// two-kernel path in a per-device scratch of the library (kPrefillDropinScratchBytes)
+// when its images fit, ordered between launches by an event.
 constexpr int64_t kPrefillDropinScratchBytes = int64_t(128) << 20;
 constexpr int64_t kDropinTwoKernelTokens = 1024;
 hipError_t launch_prefill_dropin(const PrefillArgs& args, hipStream_t stream);

@@ -2597,15 +2597,20 @@ int64_t prefill_static_device_bytes() {
   return int64_t(sizeof(scratch)) + int64_t(sizeof(dropin_scratch)) + int64_t(sizeof(gdn_prefill_giveup_count));
 }
 
-// The drop-in gdn_prefill.  One sequence of at least kDropinTwoKernelTokens tokens,
-// whose chains the launcher splits 4 or 8 ways, runs on the two-kernel path (each
-// chunk prepared once) in dropin_scratch when its images fit; everything else, and
-// any launch on a stream that is being captured into a graph, runs launch_prefill as
-// is.  Launches on the scratch are ordered on the device (launch_ordered), so calls on
-// any streams stay correct, and calls on one stream wait for nothing they would not
-// wait for anyway.
+// The drop-in gdn_prefill.  A batch of N sequences averaging at least
+// kDropinTwoKernelTokens tokens (T >= kDropinTwoKernelTokens N), whose chains the
+// launcher splits 4 or 8 ways, runs on the two-kernel path (each chunk prepared once)
+// in dropin_scratch when its images fit; everything else, and any launch on a stream
+// that is being captured into a graph, runs launch_prefill as is.  (The host sees N
+// and T, not the lengths; measured, one kernel against two, µs: [2048, 2048] 111.2 /
+// 99.2, [300, 4000] 189.4 / 150.2, [1000, 1100] 62.2 / 59.8, [900, 1200, 100, 3000]
+// at 16 v-heads 142.2 / 114.0, and below the threshold [600, 700] 42.5 / 42.4,
+// [512] x 4 at 16 v-heads 32.7 / 36.9.)  Launches on the scratch are ordered on the
+// device (launch_ordered), so calls on any streams stay correct, and calls on one
+// stream wait for nothing they would not wait for anyway.
 hipError_t launch_prefill_dropin(const PrefillArgs& a, hipStream_t stream) {
-  const int64_t need = a.N == 1 && a.T >= kDropinTwoKernelTokens ? prefill_workspace_bytes(a.N, a.T, a.Hv) : 0;
+  const int64_t need =
+      a.N >= 1 && a.T >= kDropinTwoKernelTokens * a.N ? prefill_workspace_bytes(a.N, a.T, a.Hv) : 0;
   if (need <= 0 || need > kPrefillDropinScratchBytes || a.spin_limit != 0 || a.ready_chunks != 0 ||
       a.aborts != nullptr || a.tiles != nullptr)
     return launch_prefill(a, stream);

@@ -160,15 +160,17 @@ int64_t gdn_static_device_bytes(void);
  *             so malformed offsets cannot make the kernel read out of bounds.
  *   output    [T,Hv,128] bf16
  *   new_state [N,Hv,128,128] fp32 final states; may alias state.
- * Nothing is allocated per call.  One sequence (num_seqs == 1) of at least 1,024
- * tokens, whose chains the launcher splits over several workgroups, runs the
+ * Nothing is allocated per call.  A batch whose sequences average at least 1,024
+ * tokens (total_tokens >= 1,024 num_seqs) and whose chains the launcher splits over
+ * several workgroups (at most 64 (sequence, v-head) chains on 256 CUs) runs the
  * two-kernel path of gdn_prefill_with_workspace (each chunk prepared once) in a
  * scratch array the library holds on each device (GDN_PREFILL_DROPIN_SCRATCH_BYTES,
- * its own, not gdn_prefill_no_alloc's), when its chunk images fit: 19,200 bytes per
- * 64-token chunk and v-head, so with 32 v-heads sequences of up to 13,952 tokens
- * (BASELINE's 4,096-token sequence needs 37.5 MiB).  Longer sequences run one
- * kernel (16,384 tokens: about 8 % slower than two).  The results are the same bit
- * for bit either way.  The library orders those launches on the device (each
+ * its own, not gdn_prefill_no_alloc's), when its chunk images fit:
+ * gdn_prefill_workspace_size(num_seqs, total_tokens, Hv) bytes, 19,200 per 64-token
+ * chunk and v-head of each sequence's ceil(total_tokens / 64) chunk slots, so with
+ * one sequence and 32 v-heads up to 13,952 tokens (BASELINE's 4,096-token sequence
+ * needs 37.5 MiB).  Larger batches run one kernel (one 16,384-token sequence: about
+ * 8 % slower than two).  The results are the same bit for bit either way.  The library orders those launches on the device (each
  * waits, on its stream, for an event that the previous one records as it
  * completes), so calls on any streams stay correct; on a stream that is being
  * captured into a graph such a call runs one kernel instead.
