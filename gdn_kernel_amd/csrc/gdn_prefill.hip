@@ -516,9 +516,23 @@ constexpr int kSpinLimit = 1 << 21;  // default polls (about 70 ms) before a wai
 // program order.  Nothing is published through these counters in global memory.
 template <class Smem>
 __device__ __forceinline__ void signal_count(Smem& sm, int which, int lane) {
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
-  if (lane == 0) __hip_atomic_fetch_add(&sm.sync[which], 1, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_WORKGROUP);
-  __atomic_signal_fence(__ATOMIC_SEQ_CST);
+  (void)lane;
+  // One LDS add from lane 0, with exec set to that lane inside one asm block rather
+  // than by a branch, so that the surrounding arithmetic is still scheduled as one
+  // block.  Every caller runs with the whole wave active.  The block writes no SCC
+  // (s_mov only), and the compiler does not count its LDS operation in its waits, which
+  // can only make those stricter (a wave's LDS operations complete in order).
+  typedef __attribute__((address_space(3))) int lds_int;
+  const uint32_t addr = uint32_t(reinterpret_cast<uintptr_t>((lds_int*)(&sm.sync[which])));
+  uint64_t saved;
+  asm volatile(
+      "s_mov_b64 %0, exec\n\t"
+      "s_mov_b64 exec, 1\n\t"
+      "ds_add_u32 %1, %2\n\t"
+      "s_mov_b64 exec, %0"
+      : "=&s"(saved)
+      : "v"(addr), "v"(1)
+      : "memory");
 }
 
 // Waits until counter `which` reaches `target`.  Every wait is bounded: if one
