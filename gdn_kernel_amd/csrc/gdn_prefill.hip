@@ -1975,9 +1975,13 @@ __device__ __forceinline__ void consumer_loop_tsplit(PrefillSmem& sm, const Pref
     // Output block ct: o^T = scale e^gamma (S Q^T) + v_new^T (scale P)^T.
     xq = mfma(pack_hi(Vn[0], Vn[1]), pq0, xq);
     if (ct >= 2) xq = mfma(pack_hi(Vn[2], Vn[3]), pq1, xq);
-    if (16 * ct + n16 < clen)
-      *reinterpret_cast<uint2*>(p.out + cs * vstride + (int64_t(h) * D + row0) + orow) =
-          uint2{pack_bf16x2(xq[0], xq[1]), pack_bf16x2(xq[2], xq[3])};
+    // Rows at or past clen fall outside the buffer resource, whose extent ends at the
+    // chunk's last token: the hardware drops their stores (no per-lane branch).
+    {
+      const BufferRsrc orsrc =
+          buffer_rsrc(p.out + cs * vstride + (int64_t(h) * D + row0), uint32_t(clen) * uint32_t(vstride) * 2u);
+      buffer_store8(u32x2{pack_bf16x2(xq[0], xq[1]), pack_bf16x2(xq[2], xq[3])}, orsrc, 2 * orow);
+    }
   }
 }
 
