@@ -142,9 +142,8 @@ using PersistVariant = Variant<4, 2, HOOKS, false, 4, true>;
 // The prep kernel of the two-kernel path: the four producer waves alone (no
 // consumers, no V staging); they copy each chunk's tiles out themselves (kCopy).
 struct PrepVariant {
-  static constexpr bool kHooks = false, kLoad = false, kCopy = true, kPipelined = false, kPersist = false,
-                        kTokenSplit = false;
-  static constexpr int NCW = 0, NP = 4, VT = 1, VW = 16, ROWS = 128, F = 1;
+  static constexpr bool kHooks = false, kCopy = true, kPipelined = false, kPersist = false;
+  static constexpr int NCW = 0, NP = 4, ROWS = 128, F = 1;
   static constexpr int NTHREADS = 64 * (NCW + 4);
   static constexpr int VSEG = 0;
 };
