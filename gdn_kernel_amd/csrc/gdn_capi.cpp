@@ -238,7 +238,7 @@ int decode_pooled_impl(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v, 
 }
 
 // Launcher of a prefill call: launch_prefill (optionally with a caller workspace),
-// the drop-in's (its own ordered scratch for one long sequence) or
+// the drop-in's (its own ordered scratch for batches of long sequences) or
 // gdn_prefill_no_alloc's (the library's ordered scratch).
 enum class PrefillPath { kPlain, kDropin, kNoAlloc };
 

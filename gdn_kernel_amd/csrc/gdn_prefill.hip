@@ -2527,7 +2527,7 @@ int device_cus() {
 // copy until the process ends; every call on a device shares it.
 static __device__ __align__(256) uint8_t scratch[kPrefillScratchBytes];
 
-// Scratch of the drop-in gdn_prefill's two-kernel path (one long sequence, below):
+// Scratch of the drop-in gdn_prefill's two-kernel path (long sequences, below):
 // its own array, so that no call of gdn_prefill_no_alloc, captured or not, shares it.
 static __device__ __align__(256) uint8_t dropin_scratch[kPrefillDropinScratchBytes];
 
