@@ -385,6 +385,39 @@ def test_prefill_two_kernel_path(gpu, lens, heads):
     assert_close(host(s2), s_ref, STATE_RTOL, STATE_ATOL, "new_state")
 
 
+@pytest.mark.parametrize("seed", [0, 4, 5, 9, 24, 28, 30])   # heads 4, 8, 16 and 32 v-heads, 1-3 sequences
+def test_prefill_dropin_random_long_batches(gpu, seed):
+    """Seeded random batches that gdn_prefill runs on its two-kernel path (at most 64
+    chains whose sequences average at least 1,024 tokens, images within its scratch):
+    1-3 sequences of 1-2,000 tokens topped up to that average, random head layouts, gate
+    regime, initial states and cu_seqlens dtype.  gdn_prefill equals
+    gdn_prefill_with_workspace bit for bit, both match the oracle, and no hand-off gives
+    up."""
+    rng = np.random.default_rng(3000 + seed)
+    hq, hk, hv = [(16, 16, 32), (8, 8, 16), (4, 8, 8), (2, 2, 4), (4, 4, 16)][int(rng.integers(0, 5))]
+    n = min(int(rng.integers(1, 4)), 64 // hv)
+    lens = [int(rng.integers(1, 2001)) for _ in range(n)]
+    short = 1024 * n - sum(lens)
+    if short > 0:
+        lens[int(rng.integers(0, n))] += short
+    gate = "slow" if rng.random() < 0.5 else "baseline"
+    with_state = bool(rng.random() < 0.7)
+    cu_dtype = torch.int64 if rng.random() < 0.5 else torch.int32
+    say(f"prefill drop-in random long batch seed={seed} lens={lens} heads=({hq},{hk},{hv}) gate={gate} "
+        f"state={with_state} cu={cu_dtype}")
+    p = workloads.prefill_inputs(lens, Heads(hq, hk, hv), seed=4000 + seed, gate=gate,
+                                 state_scale=0.5 if gate == "slow" else 0.05, with_state=with_state,
+                                 cu_dtype=cu_dtype)
+    binding.prefill_giveups(reset=True)
+    o1, s1 = _prefill_capi(p, gpu, workspace=False)
+    o2, s2 = _prefill_capi(p, gpu, workspace=True)
+    assert torch.equal(o1, o2) and torch.equal(s1, s2), "gdn_prefill differs from gdn_prefill_with_workspace"
+    o_ref, s_ref = oracle_prefill(p)
+    assert_close(host(o1), o_ref, OUT_RTOL, OUT_ATOL, "output")
+    assert_close(host(s1), s_ref, STATE_RTOL, STATE_ATOL, "new_state")
+    assert binding.prefill_giveups() == 0
+
+
 def test_prefill_workspace_reuse(gpu):
     """One workspace buffer, not cleared between calls, serves two different few-chain
     batches in turn (the larger first, then a smaller one whose images overlay the
