@@ -21,6 +21,7 @@ GDN_INDEX_INT64 = 1
 GDN_MAX_HEADS = 65536
 GDN_PREFILL_NO_ALLOC_SCRATCH_BYTES = 64 << 20
 GDN_PREFILL_DROPIN_SCRATCH_BYTES = 128 << 20
+GDN_PREFILL_DROPIN_TWO_KERNEL_TOKENS = 1024
 
 # Exported symbols and their argument types (must match include/gdn_kernel_amd.h and
 # include/gdn_kernel_amd_testing.h).

@@ -39,6 +39,8 @@ static_assert(GDN_PREFILL_NO_ALLOC_SCRATCH_BYTES == gdn::kPrefillScratchBytes,
               "the header's scratch size must match the library's");
 static_assert(GDN_PREFILL_DROPIN_SCRATCH_BYTES == gdn::kPrefillDropinScratchBytes,
               "the header's drop-in scratch size must match the library's");
+static_assert(GDN_PREFILL_DROPIN_TWO_KERNEL_TOKENS == gdn::kDropinTwoKernelTokens,
+              "the header's drop-in two-kernel threshold must match the library's");
 
 int check_heads(int32_t hq, int32_t hk, int32_t hv, int32_t dk, int32_t dv) {
   if (hq <= 0 || hk <= 0 || hv <= 0)

@@ -160,8 +160,9 @@ int64_t gdn_static_device_bytes(void);
  *             so malformed offsets cannot make the kernel read out of bounds.
  *   output    [T,Hv,128] bf16
  *   new_state [N,Hv,128,128] fp32 final states; may alias state.
- * Nothing is allocated per call.  A batch whose sequences average at least 1,024
- * tokens (total_tokens >= 1,024 num_seqs) and whose chains the launcher splits over
+ * Nothing is allocated per call.  A batch whose sequences average at least
+ * GDN_PREFILL_DROPIN_TWO_KERNEL_TOKENS (1,024) tokens (total_tokens >= 1,024
+ * num_seqs) and whose chains the launcher splits over
  * several workgroups (at most 64 (sequence, v-head) chains on 256 CUs) runs the
  * two-kernel path of gdn_prefill_with_workspace (each chunk prepared once) in a
  * scratch array the library holds on each device (GDN_PREFILL_DROPIN_SCRATCH_BYTES,
@@ -176,6 +177,7 @@ int64_t gdn_static_device_bytes(void);
  * captured into a graph such a call runs one kernel instead.
  */
 #define GDN_PREFILL_DROPIN_SCRATCH_BYTES (128LL << 20)
+#define GDN_PREFILL_DROPIN_TWO_KERNEL_TOKENS 1024
 
 int gdn_prefill(const gdn_bf16* q, const gdn_bf16* k, const gdn_bf16* v,
                 const float* state, const float* A_log, const gdn_bf16* a,

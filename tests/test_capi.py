@@ -118,7 +118,8 @@ def test_header_constants_match_the_python_binding():
     text = open(os.path.join(root, "include", "gdn_kernel_amd.h")).read()
     defs = dict(re.findall(r"^#define (GDN_[A-Z0-9_]+) \(?([0-9LL <]+?)\)?\s*(?:/\*.*)?$", text, re.M))
     assert {"GDN_OK", "GDN_ERR_UNSUPPORTED", "GDN_INDEX_INT64", "GDN_MAX_HEADS",
-            "GDN_PREFILL_NO_ALLOC_SCRATCH_BYTES", "GDN_PREFILL_DROPIN_SCRATCH_BYTES"} <= set(defs)
+            "GDN_PREFILL_NO_ALLOC_SCRATCH_BYTES", "GDN_PREFILL_DROPIN_SCRATCH_BYTES",
+            "GDN_PREFILL_DROPIN_TWO_KERNEL_TOKENS"} <= set(defs)
     for name, value in defs.items():
         parts = [int(x.strip().rstrip("L")) for x in value.split("<<")]
         expected = parts[0] << parts[1] if len(parts) == 2 else parts[0]
